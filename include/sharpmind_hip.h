@@ -1,0 +1,168 @@
+/*
+ * sharpmind_hip.h — C ABI of libsharpmind_hip, the MI355X (gfx950) backward-pass
+ * backend for SharpMind's autograd training stack.
+ *
+ * Conventions
+ *  - Every entry returns int: SMHIP_OK (0) or a negative SMHIP_E* code; the
+ *    message is available from smhip_last_error() on the calling thread.
+ *  - "Device" entries take device pointers (hipMalloc'd memory) and an explicit
+ *    stream (hipStream_t passed as void*, NULL = the default stream).  They are
+ *    asynchronous.  "smhip_host_*" entries take host pointers, copy in/out and
+ *    synchronise; they are the drop-in parity path for the C# P/Invoke shim.
+ *  - All matrices are row-major.  Parameter gradients are ACCUMULATED (+=),
+ *    returned activations gradients (dX) are OVERWRITTEN, exactly as the
+ *    reference's GradientMapping contract (SharpMind.Core/Training/
+ *    GradientMapping.cs:7-16).
+ *  - Thread safety: entries are re-entrant.  Internal scratch is keyed by stream;
+ *    calls issued concurrently from several threads must use distinct streams.
+ */
+#ifndef SHARPMIND_HIP_H
+#define SHARPMIND_HIP_H
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SMHIP_OK 0
+#define SMHIP_EINVAL (-1)
+#define SMHIP_EHIP (-2)
+#define SMHIP_ENOMEM (-3)
+#define SMHIP_EUNSUPPORTED (-4)
+
+/* GEMM arithmetic: fp32 MFMA (exactness mode) or bf16 MFMA with fp32 accumulate. */
+#define SMHIP_PREC_FP32 0
+#define SMHIP_PREC_BF16 1
+
+/* Quantised weight formats (values follow the reference QuantDType enum, QuantDType.cs). */
+#define SMHIP_QTYPE_F32 0
+#define SMHIP_QTYPE_Q8_0 8
+#define SMHIP_QTYPE_Q4_K 12
+
+typedef void* smhip_stream_t;
+
+/* ---------------------------------------------------------------- runtime */
+const char* smhip_last_error(void);
+int smhip_version(void);
+/* Number of visible HIP devices (0 when no GPU). */
+int smhip_device_count(void);
+
+/* ---------------------------------------------------------------- GradientMapping slots
+ * (SharpMind.Core/Training/GradientMapping.cs:26-106, keys SharpMindConfig.cs:35-41) */
+
+/* gradlinear -> GradientMapping.Linear (GradientMapping.cs:26-34, GradientKernels.cs:50-291).
+ * dY [M,Out], X [M,In], W [Out,In].  dX [M,In] = dY W (overwritten, may be NULL);
+ * dW [Out,In] += dY^T X (may be NULL); db [Out] += sum_rows dY (may be NULL). */
+int smhip_grad_linear(const float* dY, const float* X, const float* W, float* dW, float* db,
+                      float* dX, int M, int In, int Out, int precision, smhip_stream_t stream);
+
+/* gradrmsnorm -> GradientMapping.RMSNorm (GradientMapping.cs:41-48, GradientKernels.cs:303-337).
+ * xNorm [T,D] = x*rmsInv saved by forward; dw [D] += (may be NULL: frozen weight). */
+int smhip_grad_rmsnorm(const float* dY, const float* xNorm, const float* rmsInv, const float* w,
+                       float* dw, float* dX, int T, int D, smhip_stream_t stream);
+
+/* gradlayernorm -> GradientMapping.LayerNorm (GradientMapping.cs:54-62, GradientKernels.cs:345-398). */
+int smhip_grad_layernorm(const float* dY, const float* x, const float* w, float* dw, float* db,
+                         float* dX, int T, int D, float eps, smhip_stream_t stream);
+
+/* gradattention -> GradientMapping.Attention (GradientMapping.cs:68-77, GradientKernels.cs:408-481).
+ * One head with materialised probs [S,S]; dQ/dK/dV [S,D] overwritten. */
+int smhip_grad_attention(const float* dO, const float* q, const float* k, const float* v,
+                         const float* probs, float* dQ, float* dK, float* dV, int S, int D,
+                         float scale, smhip_stream_t stream);
+
+/* gradembedding -> GradientMapping.Embedding (GradientMapping.cs:84-90, GradientKernels.cs:490-506).
+ * dE [V,D] += scatter of dY [T,D] rows by ids [T]; deterministic (rows summed in token order). */
+int smhip_grad_embedding(const float* dY, const int32_t* ids, float* dE, int T, int D, int V,
+                         smhip_stream_t stream);
+
+/* gradactivationsilu / gradactivationgelu (GradientMapping.cs:92-106, GradientKernels.cs:559-675). */
+int smhip_grad_silu(const float* dY, const float* x, float* dX, int64_t n, smhip_stream_t stream);
+int smhip_grad_gelu(const float* dY, const float* x, float* dX, int64_t n, smhip_stream_t stream);
+
+/* ---------------------------------------------------------------- TrainingOps slots
+ * (SharpMind.Training/TrainingOps.cs:17-33, keys SharpMindConfig.cs:32-33) */
+
+/* adamw -> TrainingOps.AdamWUpdate (TrainingKernels.cs:19-89).  In place on data/m/v. */
+int smhip_adamw_update(float* data, const float* grad, float* m, float* v, int64_t n, float beta1,
+                       float beta2, float bc1, float bc2, float lr, float eps, float decay,
+                       smhip_stream_t stream);
+/* gradnorm -> TrainingOps.L2NormSq (TrainingKernels.cs:94-135).  *out (device float) = sum x^2,
+ * accumulated in double, deterministic. */
+int smhip_l2normsq(const float* data, int64_t n, float* out, smhip_stream_t stream);
+/* Gradients.ClipGlobalNorm's scale step (Gradients.cs:92-116): x *= scale for n elements. */
+int smhip_scale_inplace(float* x, int64_t n, float scale, smhip_stream_t stream);
+
+/* ---------------------------------------------------------------- QuantizationOps slots
+ * QuantizedMatMulFn(float* in, byte* rawW, float* out, int M, int K, int N)
+ * (QuantizationOps.cs:8-9; qmatmul_f32 :466-475, qmatmul_q8_0 :204-213, qmatmul_q4k :400-409).
+ * out[M,N] = in[M,K] . W^T with W rows [N][K] in the reference byte layout. */
+int smhip_qmatmul(int qtype, const float* in, const void* rawW, float* out, int M, int K, int N,
+                  int precision, smhip_stream_t stream);
+
+/* Bit-exact dequantisation of a reference-layout stream of n elements
+ * (ReadQ8_0_Scalar QuantizationKernels.Q8.cs:412-433, ReadQ4K_Scalar QuantizationKernels.Q4.cs:951-981). */
+int smhip_dequant(int qtype, const void* raw, float* out, int64_t n, smhip_stream_t stream);
+
+/* ---------------------------------------------------------------- BackpropEngine inline math
+ * (no slot in the reference; these restate loops in SharpMind.Training/Autograd/BackpropEngine.cs) */
+
+/* SwiGLU backward (BackpropEngine.cs:623-657): dAct, gate, up [T,F] -> dFused [T,2F] = [dGate | dUp]. */
+int smhip_grad_swiglu(const float* dAct, const float* gate, const float* up, float* dFused, int T,
+                      int F, smhip_stream_t stream);
+/* SwiGLU forward act = silu(gate)*up (ActivationKernels.cs:194-205). */
+int smhip_swiglu_forward(const float* gate, const float* up, float* act, int64_t n,
+                         smhip_stream_t stream);
+
+/* RoPE tables (RoPE.cs:99-148, no scaling): host arrays cosT/sinT [maxSeq, ropeDim/2]. */
+int smhip_rope_tables(float theta, int ropeDim, int maxSeq, float* cosT, float* sinT);
+/* RoPE forward / backward in place on x [B,S,H,D] with device tables (RoPE.cs:168-347);
+ * neox != 0 pairs (d, d+D/2), else adjacent (2i, 2i+1). */
+int smhip_rope_forward(float* x, const float* cosT, const float* sinT, int B, int S, int H, int D,
+                       int neox, smhip_stream_t stream);
+int smhip_rope_backward(float* dx, const float* cosT, const float* sinT, int B, int S, int H, int D,
+                        int neox, smhip_stream_t stream);
+
+/* RMSNorm forward with state (NormLayer.cs:72-89, NormKernels.cs:13-60): y = x*rmsInv*w. */
+int smhip_rmsnorm_forward(const float* x, const float* w, float* y, float* rmsInv, int T, int D,
+                          float eps, smhip_stream_t stream);
+
+/* Combined softmax + cross-entropy gradient (Gradients.cs:33-84) and loss
+ * (CrossEntropyLoss.cs:44-104).  dLogits [T,V] overwritten (may alias logits);
+ * loss (device float, may be NULL) = mean over labels != ignoreId. */
+int smhip_ce_softmax_grad(const float* logits, const int32_t* labels, float* dLogits, float* loss,
+                          int T, int V, int ignoreId, float smoothing, smhip_stream_t stream);
+
+/* Causal attention forward with materialised probs (BackpropEngine.cs:237-388, exact-exp path):
+ * q [B,S,Hq,D], k/v [B,S,Hkv,D] -> probs [B,Hq,S,S], out [B,S,Hq*D]. */
+int smhip_attention_forward_probs(const float* q, const float* k, const float* v, float* probs,
+                                  float* out, int B, int S, int Hq, int Hkv, int D,
+                                  smhip_stream_t stream);
+
+/* ---------------------------------------------------------------- host-pointer slot entries
+ * Same semantics as the device entries above, on host memory (synchronous).  These are
+ * what SharpMind.HIP's [PuzzlePeice] methods P/Invoke. */
+int smhip_host_grad_linear(const float* dY, const float* X, const float* W, float* dW, float* db,
+                           float* dX, int M, int In, int Out, int precision);
+int smhip_host_grad_rmsnorm(const float* dY, const float* xNorm, const float* rmsInv,
+                            const float* w, float* dw, float* dX, int T, int D);
+int smhip_host_grad_layernorm(const float* dY, const float* x, const float* w, float* dw,
+                              float* db, float* dX, int T, int D, float eps);
+int smhip_host_grad_attention(const float* dO, const float* q, const float* k, const float* v,
+                              const float* probs, float* dQ, float* dK, float* dV, int S, int D,
+                              float scale);
+int smhip_host_grad_embedding(const float* dY, const int32_t* ids, float* dE, int T, int D, int V);
+int smhip_host_grad_silu(const float* dY, const float* x, float* dX, int64_t n);
+int smhip_host_grad_gelu(const float* dY, const float* x, float* dX, int64_t n);
+int smhip_host_adamw_update(float* data, const float* grad, float* m, float* v, int64_t n,
+                            float beta1, float beta2, float bc1, float bc2, float lr, float eps,
+                            float decay);
+int smhip_host_l2normsq(const float* data, int64_t n, float* out);
+int smhip_host_qmatmul(int qtype, const float* in, const void* rawW, float* out, int M, int K,
+                       int N);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

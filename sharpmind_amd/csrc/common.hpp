@@ -1,0 +1,152 @@
+// common.hpp — shared device/host helpers for libsharpmind_hip (gfx950 / CDNA4).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+#include <mutex>
+#include <unordered_map>
+
+#include "../../include/sharpmind_hip.h"
+
+namespace smhip {
+
+// ---------------------------------------------------------------- errors
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+
+#define SMHIP_CHECK_HIP(expr)                                                        \
+  do {                                                                               \
+    hipError_t _e = (expr);                                                          \
+    if (_e != hipSuccess)                                                            \
+      return ::smhip::fail(SMHIP_EHIP, std::string(#expr) + ": " + hipGetErrorString(_e)); \
+  } while (0)
+
+#define SMHIP_REQUIRE(cond, msg) \
+  do { if (!(cond)) return ::smhip::fail(SMHIP_EINVAL, msg); } while (0)
+
+// Launch-error check: reports the launch error (not a later fault).
+#define SMHIP_CHECK_LAUNCH() SMHIP_CHECK_HIP(hipGetLastError())
+
+// ---------------------------------------------------------------- workspace
+// Per-stream growable device scratch.  Calls on one stream are ordered, so a
+// buffer keyed by stream is never used by two kernels at once; calls from
+// different threads must use different streams (documented in the header).
+void* workspace(hipStream_t s, size_t bytes, int slot = 0);
+
+// ---------------------------------------------------------------- bf16
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// float -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __host__ inline uint16_t f2bf(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __host__ inline float bf2f(uint16_t b) {
+  return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+__device__ inline uint32_t pack_bf2(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+// Bit-exact IEEE half -> float (every binary16 value is exact in binary32),
+// same result as HalfToFloat_Scalar (QuantizationKernels.cs:117-146).
+__device__ __host__ inline float half_bits_to_float(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+  uint32_t bits;
+  if (e == 0) {
+    if (m == 0) {
+      bits = sign;
+    } else {
+      int k = 31 - __builtin_clz(m);  // msb position, 0..9
+      bits = sign | ((uint32_t)(k + 103) << 23) | ((m - (1u << k)) << (23 - k));
+    }
+  } else if (e == 31) {
+    bits = m ? 0x7FC00000u : (sign | 0x7F800000u);
+  } else {
+    bits = sign | ((e + 112) << 23) | (m << 13);
+  }
+  return __builtin_bit_cast(float, bits);
+}
+
+// ---------------------------------------------------------------- reductions (wave64)
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ inline double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+inline int num_cus() {
+  static int n = 0;
+  if (!n) {
+    int dev = 0;
+    hipGetDevice(&dev);
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, dev) == hipSuccess) n = p.multiProcessorCount;
+    if (n <= 0) n = 256;
+  }
+  return n;
+}
+
+// ---------------------------------------------------------------- GEMM operand descriptor
+// Element (r, k) of an operand tile, r = row of A (m) or column of B (n).
+enum SrcMode : int {
+  SRC_F32_K = 0,   // float, p[r*ld + k]
+  SRC_F32_R = 1,   // float, p[k*ld + r]
+  SRC_BF16_K = 2,  // bf16,  p[r*ld + k]
+  SRC_BF16_R = 3,  // bf16,  p[k*ld + r]
+  SRC_Q8_K = 4,    // repacked Q8_0 planes, flat element e = r*ld + k
+  SRC_Q8_R = 5,    // repacked Q8_0 planes, flat element e = k*ld + r
+  SRC_Q4K_K = 6,   // repacked Q4_K planes, e = r*ld + k
+  SRC_Q4K_R = 7,   // repacked Q4_K planes, e = k*ld + r
+};
+
+struct Operand {
+  int mode;
+  const void* p;       // dense data, or quant value plane (int8 for Q8, packed nibbles for Q4_K)
+  const float* s;      // Q8: fp32 scale per 32-element block; Q4K: (s*d, m*dmin) float pairs per 32
+  int64_t ld;          // row length in elements of the stored matrix
+};
+
+// Repacked quantized weight (device planes).  Q8_0: qs int8 [n], d f32 [n/32].
+// Q4_K: qs uint8 [n/2] in Q4_K nibble order, sm float2 [n/32] = (sc*d, mn*dmin).
+struct QuantPlanes {
+  int kind;  // SMHIP_QTYPE_*
+  int64_t n;
+  void* qs;
+  float* sc;
+};
+
+// GEMM: C[M,N] = alpha * op(A) op(B)^T + beta * C  (beta 0 or 1), optional second
+// (rank-extension) pair A2 [M,K2] bf16/f32 and B2 so that C += alpha2 * A2 B2^T.
+struct GemmArgs {
+  int M, N, K;
+  Operand A, B;
+  int K2;              // 0 = no extension
+  Operand A2, B2;
+  float alpha, alpha2, beta;
+  void* C;
+  int64_t ldc;
+  int c_bf16;          // output stored as bf16
+  int precision;       // SMHIP_PREC_FP32 | SMHIP_PREC_BF16
+  int split_k;         // >1: deterministic split-K through workspace
+};
+int gemm(const GemmArgs& g, hipStream_t s);
+
+}  // namespace smhip

@@ -1,0 +1,921 @@
+// elementwise.hip — bandwidth-bound training kernels for gfx950.
+//
+// Every kernel here is HBM-bound: one pass over its operands with 16-byte
+// vector loads, wave64 shuffle reductions for per-row statistics, and
+// deterministic two-stage reductions (per-block partials in a fixed order)
+// wherever the reference sums across rows, so results are run-to-run
+// identical.  The library is compiled with -ffp-contract=off so per-element
+// arithmetic rounds in the same order as the reference's scalar C# loops.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace smhip {
+
+static constexpr int kBlock = 256;
+
+__device__ inline float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ inline void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+
+static int grid_for(int64_t work_items, int per_block, int max_blocks_per_cu = 8) {
+  int64_t g = (work_items + per_block - 1) / per_block;
+  int64_t cap = (int64_t)num_cus() * max_blocks_per_cu;
+  if (g > cap) g = cap;
+  if (g < 1) g = 1;
+  return (int)g;
+}
+
+// ============================================================================
+// RMSNorm backward (GradientKernels.RMSNorm_Scalar, GradientKernels.cs:303-337)
+//   dw += sum_t dy*xn ; dot = sum_d dy*w*xn / D ; dx = ri*(dy*w - xn*dot)
+// One wave per row; each lane owns VEC-wide column groups, NCH groups per row.
+// xn is either given (slot form) or rebuilt as x*rinv (engine form).
+// ============================================================================
+template <int VEC, int NCH, bool FROM_X, bool HAS_DW>
+__global__ __launch_bounds__(kBlock) void rmsnorm_bwd_kernel(
+    const float* __restrict__ dY, const float* __restrict__ xin, const float* __restrict__ rinv,
+    const float* __restrict__ w, float* __restrict__ dX, float* __restrict__ dw_part, int T, int D,
+    int accumulate, uint16_t* __restrict__ dX_bf16) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int waves = kBlock / 64;
+  float acc[NCH][VEC];
+#pragma unroll
+  for (int c = 0; c < NCH; c++)
+#pragma unroll
+    for (int v = 0; v < VEC; v++) acc[c][v] = 0.f;
+
+  for (int t = blockIdx.x * waves + wv; t < T; t += gridDim.x * waves) {
+    const float* dy = dY + (int64_t)t * D;
+    const float* xr = xin + (int64_t)t * D;
+    const float ri = rinv[t];
+    float yv[NCH][VEC], xv[NCH][VEC], wv_[NCH][VEC];
+    float dot = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+      const int col = (c * 64 + lane) * VEC;
+      if (col < D) {
+        if constexpr (VEC == 4) {
+          float4 a = ld4(dy + col), b = ld4(xr + col), g = ld4(w + col);
+          yv[c][0] = a.x; yv[c][1] = a.y; yv[c][2] = a.z; yv[c][3] = a.w;
+          xv[c][0] = b.x; xv[c][1] = b.y; xv[c][2] = b.z; xv[c][3] = b.w;
+          wv_[c][0] = g.x; wv_[c][1] = g.y; wv_[c][2] = g.z; wv_[c][3] = g.w;
+        } else {
+          yv[c][0] = dy[col]; xv[c][0] = xr[col]; wv_[c][0] = w[col];
+        }
+#pragma unroll
+        for (int v = 0; v < VEC; v++) {
+          if (FROM_X) xv[c][v] = xv[c][v] * ri;
+          if (HAS_DW) acc[c][v] += yv[c][v] * xv[c][v];
+          dot += yv[c][v] * wv_[c][v] * xv[c][v];
+        }
+      }
+    }
+    dot = wave_sum(dot) / (float)D;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+      const int col = (c * 64 + lane) * VEC;
+      if (col < D) {
+        float o[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; v++) o[v] = ri * (yv[c][v] * wv_[c][v] - xv[c][v] * dot);
+        float* dst = dX + (int64_t)t * D + col;
+        if (accumulate) {
+#pragma unroll
+          for (int v = 0; v < VEC; v++) o[v] = dst[v] + o[v];
+        }
+        if constexpr (VEC == 4) st4(dst, make_float4(o[0], o[1], o[2], o[3]));
+        else dst[0] = o[0];
+        if (dX_bf16) {
+#pragma unroll
+          for (int v = 0; v < VEC; v++) dX_bf16[(int64_t)t * D + col + v] = f2bf(o[v]);
+        }
+      }
+    }
+  }
+  if constexpr (HAS_DW) {
+    // combine the block's waves in fixed order through LDS, one partial row per block
+    extern __shared__ float sh[];  // [waves][D]
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+      const int col = (c * 64 + lane) * VEC;
+      if (col < D)
+#pragma unroll
+        for (int v = 0; v < VEC; v++) sh[wv * D + col + v] = acc[c][v];
+    }
+    __syncthreads();
+    for (int d = threadIdx.x; d < D; d += kBlock) {
+      float s = sh[d];
+      for (int k = 1; k < waves; k++) s += sh[k * D + d];
+      dw_part[(int64_t)blockIdx.x * D + d] = s;
+    }
+  }
+}
+
+// dst[d] += sum_g part[g*D + d], g ascending (deterministic).
+__global__ void column_reduce_add_kernel(const float* __restrict__ part, float* __restrict__ dst,
+                                         int G, int D) {
+  int d = blockIdx.x * blockDim.x + threadIdx.x;
+  if (d >= D) return;
+  float s = 0.f;
+  for (int g = 0; g < G; g++) s += part[(int64_t)g * D + d];
+  dst[d] += s;
+}
+
+template <int VEC, int NCH, bool FROM_X, bool HAS_DW>
+static int rmsnorm_bwd_launch(const float* dY, const float* x, const float* rinv, const float* w,
+                              float* dw, float* dX, int T, int D, int accumulate, uint16_t* dXb,
+                              hipStream_t s) {
+  int G = grid_for(T, kBlock / 64, 2);
+  float* part = nullptr;
+  size_t shm = 0;
+  if (HAS_DW) {
+    part = (float*)workspace(s, sizeof(float) * (size_t)G * D, 0);
+    if (!part) return fail(SMHIP_ENOMEM, "rmsnorm backward: workspace");
+    shm = sizeof(float) * (kBlock / 64) * D;
+  }
+  hipLaunchKernelGGL((rmsnorm_bwd_kernel<VEC, NCH, FROM_X, HAS_DW>), dim3(G), dim3(kBlock), shm, s,
+                     dY, x, rinv, w, dX, part, T, D, accumulate, dXb);
+  SMHIP_CHECK_LAUNCH();
+  if (HAS_DW) {
+    hipLaunchKernelGGL(column_reduce_add_kernel, dim3(ceil_div(D, 256)), dim3(256), 0, s, part, dw,
+                       G, D);
+    SMHIP_CHECK_LAUNCH();
+  }
+  return SMHIP_OK;
+}
+
+template <bool FROM_X, bool HAS_DW>
+static int rmsnorm_bwd_dispatch(const float* dY, const float* x, const float* rinv, const float* w,
+                                float* dw, float* dX, int T, int D, int accumulate, uint16_t* dXb,
+                                hipStream_t s) {
+  const bool v4 = (D % 4 == 0) && ((uintptr_t)dY % 16 == 0) && ((uintptr_t)x % 16 == 0) &&
+                  ((uintptr_t)w % 16 == 0) && ((uintptr_t)dX % 16 == 0);
+  if (v4) {
+    int nch = ceil_div(D, 256);
+    if (nch <= 1) return rmsnorm_bwd_launch<4, 1, FROM_X, HAS_DW>(dY, x, rinv, w, dw, dX, T, D, accumulate, dXb, s);
+    if (nch <= 2) return rmsnorm_bwd_launch<4, 2, FROM_X, HAS_DW>(dY, x, rinv, w, dw, dX, T, D, accumulate, dXb, s);
+    if (nch <= 4) return rmsnorm_bwd_launch<4, 4, FROM_X, HAS_DW>(dY, x, rinv, w, dw, dX, T, D, accumulate, dXb, s);
+    if (nch <= 8) return rmsnorm_bwd_launch<4, 8, FROM_X, HAS_DW>(dY, x, rinv, w, dw, dX, T, D, accumulate, dXb, s);
+    return fail(SMHIP_EUNSUPPORTED, "rmsnorm backward: D > 2048");
+  }
+  int nch = ceil_div(D, 64);
+  if (nch <= 1) return rmsnorm_bwd_launch<1, 1, FROM_X, HAS_DW>(dY, x, rinv, w, dw, dX, T, D, accumulate, dXb, s);
+  if (nch <= 4) return rmsnorm_bwd_launch<1, 4, FROM_X, HAS_DW>(dY, x, rinv, w, dw, dX, T, D, accumulate, dXb, s);
+  if (nch <= 16) return rmsnorm_bwd_launch<1, 16, FROM_X, HAS_DW>(dY, x, rinv, w, dw, dX, T, D, accumulate, dXb, s);
+  return fail(SMHIP_EUNSUPPORTED, "rmsnorm backward: D not a multiple of 4 and > 1024");
+}
+
+int rmsnorm_backward(const float* dY, const float* xin, int from_x, const float* rinv,
+                     const float* w, float* dw, float* dX, int T, int D, int accumulate,
+                     uint16_t* dX_bf16, hipStream_t s) {
+  if (T <= 0 || D <= 0) return SMHIP_OK;
+  if (from_x) {
+    return dw ? rmsnorm_bwd_dispatch<true, true>(dY, xin, rinv, w, dw, dX, T, D, accumulate, dX_bf16, s)
+              : rmsnorm_bwd_dispatch<true, false>(dY, xin, rinv, w, dw, dX, T, D, accumulate, dX_bf16, s);
+  }
+  return dw ? rmsnorm_bwd_dispatch<false, true>(dY, xin, rinv, w, dw, dX, T, D, accumulate, dX_bf16, s)
+            : rmsnorm_bwd_dispatch<false, false>(dY, xin, rinv, w, dw, dX, T, D, accumulate, dX_bf16, s);
+}
+
+// ============================================================================
+// RMSNorm forward (NormKernels.cs:40-60 rmsInv = 1/sqrt(mean(x^2)+eps); :13-33 y = x*ri*w)
+// ============================================================================
+__global__ __launch_bounds__(kBlock) void rmsnorm_fwd_kernel(
+    const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y,
+    uint16_t* __restrict__ yb, float* __restrict__ rinv, int T, int D, float eps) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  for (int t = blockIdx.x * 4 + wv; t < T; t += gridDim.x * 4) {
+    const float* xr = x + (int64_t)t * D;
+    float ss = 0.f;
+    for (int d = lane; d < D; d += 64) ss += xr[d] * xr[d];
+    ss = wave_sum(ss);
+    float ri = 1.f / sqrtf(ss / (float)D + eps);
+    if (lane == 0) rinv[t] = ri;
+    for (int d = lane; d < D; d += 64) {
+      float o = xr[d] * ri * w[d];
+      if (y) y[(int64_t)t * D + d] = o;
+      if (yb) yb[(int64_t)t * D + d] = f2bf(o);
+    }
+  }
+}
+
+int rmsnorm_forward(const float* x, const float* w, float* y, uint16_t* yb, float* rinv, int T,
+                    int D, float eps, hipStream_t s) {
+  if (T <= 0) return SMHIP_OK;
+  hipLaunchKernelGGL(rmsnorm_fwd_kernel, dim3(grid_for(T, 4)), dim3(kBlock), 0, s, x, w, y, yb,
+                     rinv, T, D, eps);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// ============================================================================
+// LayerNorm backward (GradientKernels.LayerNorm_Scalar, GradientKernels.cs:345-398)
+// ============================================================================
+__global__ __launch_bounds__(kBlock) void layernorm_bwd_kernel(
+    const float* __restrict__ dY, const float* __restrict__ X, const float* __restrict__ w,
+    float* __restrict__ dX, float* __restrict__ part_w, float* __restrict__ part_b, int T, int D,
+    float eps) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  extern __shared__ float sh[];  // [2][4][D] wave partials
+  float* shw = sh;
+  float* shb = sh + 4 * D;
+  for (int d = threadIdx.x; d < 8 * D; d += kBlock) sh[d] = 0.f;
+  __syncthreads();
+  for (int t = blockIdx.x * 4 + wv; t < T; t += gridDim.x * 4) {
+    const float* x = X + (int64_t)t * D;
+    const float* dy = dY + (int64_t)t * D;
+    float mean = 0.f;
+    for (int d = lane; d < D; d += 64) mean += x[d];
+    mean = wave_sum(mean) / (float)D;
+    float var = 0.f;
+    for (int d = lane; d < D; d += 64) { float q = x[d] - mean; var += q * q; }
+    var = wave_sum(var) / (float)D;
+    float invStd = 1.f / sqrtf(var + eps);
+    float a = 0.f, b = 0.f;
+    for (int d = lane; d < D; d += 64) {
+      float xh = (x[d] - mean) * invStd;
+      shw[wv * D + d] += dy[d] * xh;
+      shb[wv * D + d] += dy[d];
+      a += dy[d] * w[d] * xh;
+      b += dy[d] * w[d];
+    }
+    a = wave_sum(a);
+    b = wave_sum(b);
+    for (int d = lane; d < D; d += 64) {
+      float xh = (x[d] - mean) * invStd;
+      dX[(int64_t)t * D + d] = invStd * (dy[d] * w[d] - (b + xh * a) / (float)D);
+    }
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += kBlock) {
+    float sw = shw[d], sb = shb[d];
+    for (int k = 1; k < 4; k++) { sw += shw[k * D + d]; sb += shb[k * D + d]; }
+    part_w[(int64_t)blockIdx.x * D + d] = sw;
+    part_b[(int64_t)blockIdx.x * D + d] = sb;
+  }
+}
+
+int layernorm_backward(const float* dY, const float* x, const float* w, float* dw, float* db,
+                       float* dX, int T, int D, float eps, hipStream_t s) {
+  if (T <= 0) return SMHIP_OK;
+  if ((size_t)8 * D * sizeof(float) > 64 * 1024) return fail(SMHIP_EUNSUPPORTED, "layernorm backward: D > 2048");
+  int G = grid_for(T, 4, 2);
+  float* part = (float*)workspace(s, sizeof(float) * (size_t)G * D * 2, 0);
+  if (!part) return fail(SMHIP_ENOMEM, "layernorm backward: workspace");
+  hipLaunchKernelGGL(layernorm_bwd_kernel, dim3(G), dim3(kBlock), 8 * D * sizeof(float), s, dY, x,
+                     w, dX, part, part + (size_t)G * D, T, D, eps);
+  SMHIP_CHECK_LAUNCH();
+  if (dw) hipLaunchKernelGGL(column_reduce_add_kernel, dim3(ceil_div(D, 256)), dim3(256), 0, s, part, dw, G, D);
+  if (db) hipLaunchKernelGGL(column_reduce_add_kernel, dim3(ceil_div(D, 256)), dim3(256), 0, s, part + (size_t)G * D, db, G, D);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// ============================================================================
+// SwiGLU (BackpropEngine.cs:623-657 backward; ActivationKernels.cs:194-205 forward)
+//   u' = da*silu(g) ; g' = da*sig*(1+g*(1-sig))*u
+// Strided rows so the engine can read gate/up out of one fused [T,2F] buffer.
+// ============================================================================
+template <typename TOut>
+__device__ inline void store_out(TOut* p, float v);
+template <> __device__ inline void store_out<float>(float* p, float v) { *p = v; }
+template <> __device__ inline void store_out<uint16_t>(uint16_t* p, float v) { *p = f2bf(v); }
+
+template <typename TIn>
+__device__ inline float load_in(const TIn* p);
+template <> __device__ inline float load_in<float>(const float* p) { return *p; }
+template <> __device__ inline float load_in<uint16_t>(const uint16_t* p) { return bf2f(*p); }
+
+template <typename TIn, typename TOut>
+__global__ __launch_bounds__(kBlock) void swiglu_bwd_kernel(
+    const TIn* __restrict__ dA, int64_t ldA, const TIn* __restrict__ G_, const TIn* __restrict__ U,
+    int64_t ldGU, TOut* __restrict__ dG, TOut* __restrict__ dU, int64_t ldOut, int T, int F) {
+  const int64_t n = (int64_t)T * F;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock) {
+    const int64_t t = i / F, d = i - t * F;
+    float g = load_in(G_ + t * ldGU + d), u = load_in(U + t * ldGU + d), da = load_in(dA + t * ldA + d);
+    float sig = 1.f / (1.f + expf(-g));
+    float gv = g * sig;
+    float gd = sig * (1.f + g * (1.f - sig));
+    store_out(dU + t * ldOut + d, da * gv);
+    store_out(dG + t * ldOut + d, da * gd * u);
+  }
+}
+
+// Contiguous fp32 fast path: rows of F floats, float4 lanes.
+__global__ __launch_bounds__(kBlock) void swiglu_bwd_v4_kernel(
+    const float* __restrict__ dA, const float* __restrict__ G_, const float* __restrict__ U,
+    float* __restrict__ out, int T, int F) {
+  const int F4 = F / 4;
+  const int64_t n4 = (int64_t)T * F4;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += (int64_t)gridDim.x * kBlock) {
+    const int64_t t = i / F4, c = (i - t * F4) * 4;
+    float4 da = ld4(dA + t * F + c), g = ld4(G_ + t * F + c), u = ld4(U + t * F + c);
+    float ga[4] = {g.x, g.y, g.z, g.w}, ua[4] = {u.x, u.y, u.z, u.w}, daa[4] = {da.x, da.y, da.z, da.w};
+    float og[4], ou[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      float sig = 1.f / (1.f + expf(-ga[v]));
+      ou[v] = daa[v] * (ga[v] * sig);
+      og[v] = daa[v] * (sig * (1.f + ga[v] * (1.f - sig))) * ua[v];
+    }
+    float* row = out + t * 2 * (int64_t)F;
+    st4(row + c, make_float4(og[0], og[1], og[2], og[3]));
+    st4(row + F + c, make_float4(ou[0], ou[1], ou[2], ou[3]));
+  }
+}
+
+int swiglu_backward_f32(const float* dAct, const float* gate, const float* up, float* dFused, int T,
+                        int F, hipStream_t s) {
+  if ((int64_t)T * F == 0) return SMHIP_OK;
+  if (F % 4 == 0 && (uintptr_t)dAct % 16 == 0 && (uintptr_t)gate % 16 == 0 &&
+      (uintptr_t)up % 16 == 0 && (uintptr_t)dFused % 16 == 0) {
+    hipLaunchKernelGGL(swiglu_bwd_v4_kernel, dim3(grid_for((int64_t)T * F / 4, kBlock)),
+                       dim3(kBlock), 0, s, dAct, gate, up, dFused, T, F);
+  } else {
+    hipLaunchKernelGGL((swiglu_bwd_kernel<float, float>), dim3(grid_for((int64_t)T * F, kBlock)),
+                       dim3(kBlock), 0, s, dAct, (int64_t)F, gate, up, (int64_t)F, dFused,
+                       dFused + F, (int64_t)2 * F, T, F);
+  }
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// Engine form: dAct fp32 [T,F]; gate/up bf16 in one fused [T,2F] row; out bf16 [T,2F].
+__global__ __launch_bounds__(kBlock) void swiglu_bwd_mixed_kernel(
+    const float* __restrict__ dA, const uint16_t* __restrict__ gu, uint16_t* __restrict__ dgu,
+    int T, int F) {
+  const int64_t n = (int64_t)T * F;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock) {
+    const int64_t t = i / F, d = i - t * F;
+    float g = bf2f(gu[t * 2 * F + d]), u = bf2f(gu[t * 2 * F + F + d]), da = dA[i];
+    float sig = 1.f / (1.f + expf(-g));
+    dgu[t * 2 * F + F + d] = f2bf(da * (g * sig));
+    dgu[t * 2 * F + d] = f2bf(da * (sig * (1.f + g * (1.f - sig))) * u);
+  }
+}
+
+int swiglu_backward_mixed(const float* dAct, const uint16_t* gu, uint16_t* dgu, int T, int F,
+                          hipStream_t s) {
+  hipLaunchKernelGGL(swiglu_bwd_mixed_kernel, dim3(grid_for((int64_t)T * F, kBlock)), dim3(kBlock),
+                     0, s, dAct, gu, dgu, T, F);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+__global__ __launch_bounds__(kBlock) void swiglu_fwd_kernel(const float* __restrict__ g,
+                                                            const float* __restrict__ u,
+                                                            float* __restrict__ a, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock) {
+    float x = g[i];
+    a[i] = (x / (1.f + expf(-x))) * u[i];
+  }
+}
+
+int swiglu_forward_f32(const float* g, const float* u, float* a, int64_t n, hipStream_t s) {
+  if (n == 0) return SMHIP_OK;
+  hipLaunchKernelGGL(swiglu_fwd_kernel, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, g, u, a, n);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// Engine form: gu bf16 [T,2F] -> act bf16 [T,F]
+__global__ __launch_bounds__(kBlock) void swiglu_fwd_bf16_kernel(const uint16_t* __restrict__ gu,
+                                                                 uint16_t* __restrict__ act, int T,
+                                                                 int F) {
+  const int64_t n = (int64_t)T * F;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock) {
+    const int64_t t = i / F, d = i - t * F;
+    float g = bf2f(gu[t * 2 * F + d]), u = bf2f(gu[t * 2 * F + F + d]);
+    act[i] = f2bf((g / (1.f + expf(-g))) * u);
+  }
+}
+
+int swiglu_forward_bf16(const uint16_t* gu, uint16_t* act, int T, int F, hipStream_t s) {
+  hipLaunchKernelGGL(swiglu_fwd_bf16_kernel, dim3(grid_for((int64_t)T * F, kBlock)), dim3(kBlock),
+                     0, s, gu, act, T, F);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// ============================================================================
+// SiLU / GELU backward (GradientKernels.cs:559-573, :612-630)
+// ============================================================================
+__global__ __launch_bounds__(kBlock) void silu_bwd_kernel(const float* __restrict__ dy,
+                                                          const float* __restrict__ x,
+                                                          float* __restrict__ dx, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock) {
+    float v = x[i];
+    float sig = 1.f / (1.f + expf(-v));
+    dx[i] = dy[i] * (sig + v * sig * (1.f - sig));
+  }
+}
+__global__ __launch_bounds__(kBlock) void gelu_bwd_kernel(const float* __restrict__ dy,
+                                                          const float* __restrict__ x,
+                                                          float* __restrict__ dx, int64_t n) {
+  const float c0 = 0.7978845608f, c1 = 0.044715f;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock) {
+    float v = x[i];
+    float x3 = v * v * v;
+    float inner = c0 * (v + c1 * x3);
+    float th = tanhf(inner);
+    float dth = 1.f - th * th;
+    float dinner = c0 * (1.f + 3.f * c1 * v * v);
+    dx[i] = dy[i] * (0.5f * (1.f + th) + 0.5f * v * dth * dinner);
+  }
+}
+
+int silu_backward(const float* dy, const float* x, float* dx, int64_t n, hipStream_t s) {
+  if (!n) return SMHIP_OK;
+  hipLaunchKernelGGL(silu_bwd_kernel, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, dy, x, dx, n);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+int gelu_backward(const float* dy, const float* x, float* dx, int64_t n, hipStream_t s) {
+  if (!n) return SMHIP_OK;
+  hipLaunchKernelGGL(gelu_bwd_kernel, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, dy, x, dx, n);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// ============================================================================
+// RoPE forward/backward in place on x [B,S,H,D] (RoPE.cs:168-259, :300-347)
+// ============================================================================
+template <bool BWD>
+__global__ __launch_bounds__(kBlock) void rope_kernel(float* __restrict__ x, const float* __restrict__ cosT,
+                                                      const float* __restrict__ sinT, int B, int S,
+                                                      int H, int D, int neox) {
+  const int pairs = D / 2;
+  const int64_t n = (int64_t)B * S * H * pairs;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock) {
+    const int p = (int)(i % pairs);
+    const int64_t row = i / pairs;  // (b*S + s)*H + h
+    const int s = (int)((row / H) % S);
+    float* v = x + row * D;
+    const int i0 = neox ? p : 2 * p, i1 = neox ? p + pairs : 2 * p + 1;
+    const float c = cosT[(int64_t)s * pairs + p], sn = sinT[(int64_t)s * pairs + p];
+    float a = v[i0], b = v[i1];
+    if (BWD) {
+      v[i0] = c * a + sn * b;
+      v[i1] = -sn * a + c * b;
+    } else {
+      v[i0] = a * c - b * sn;
+      v[i1] = b * c + a * sn;
+    }
+  }
+}
+
+int rope_apply(float* x, const float* cosT, const float* sinT, int B, int S, int H, int D, int neox,
+               int backward, hipStream_t s) {
+  int64_t n = (int64_t)B * S * H * (D / 2);
+  if (!n) return SMHIP_OK;
+  if (backward)
+    hipLaunchKernelGGL(rope_kernel<true>, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, x, cosT, sinT, B, S, H, D, neox);
+  else
+    hipLaunchKernelGGL(rope_kernel<false>, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, x, cosT, sinT, B, S, H, D, neox);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// ============================================================================
+// Cross-entropy + softmax gradient (Gradients.cs:33-84), loss (CrossEntropyLoss.cs:44-104)
+// ============================================================================
+__global__ void count_labels_kernel(const int32_t* __restrict__ labels, int T, int ignoreId,
+                                    int* __restrict__ count) {
+  __shared__ int sh[kBlock];
+  int c = 0;
+  for (int t = threadIdx.x; t < T; t += kBlock) c += labels[t] != ignoreId;
+  sh[threadIdx.x] = c;
+  __syncthreads();
+  for (int o = kBlock / 2; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) sh[threadIdx.x] += sh[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *count = sh[0];
+}
+
+// Block-wide (max, sum-exp) combine for a 1024-thread block.
+template <int NT>
+__device__ inline void block_max_sum(float& m, float& s, float* shm) {
+  // wave combine
+  for (int o = 32; o > 0; o >>= 1) {
+    float m2 = __shfl_xor(m, o, 64), s2 = __shfl_xor(s, o, 64);
+    float mn = fmaxf(m, m2);
+    s = (m == -INFINITY ? 0.f : s * expf(m - mn)) + (m2 == -INFINITY ? 0.f : s2 * expf(m2 - mn));
+    m = mn;
+  }
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) { shm[2 * wv] = m; shm[2 * wv + 1] = s; }
+  __syncthreads();
+  float M = shm[0], Ssum = 0.f;
+  for (int k = 1; k < NT / 64; k++) M = fmaxf(M, shm[2 * k]);
+  for (int k = 0; k < NT / 64; k++) {
+    float mk = shm[2 * k];
+    Ssum += mk == -INFINITY ? 0.f : shm[2 * k + 1] * expf(mk - M);
+  }
+  m = M;
+  s = Ssum;
+}
+
+template <int NT>
+__device__ inline float block_max(float v, float* shm) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) shm[wv] = v;
+  __syncthreads();
+  float r = shm[0];
+  for (int k = 1; k < NT / 64; k++) r = fmaxf(r, shm[k]);
+  return r;
+}
+template <int NT>
+__device__ inline float block_sum(float v, float* shm) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) shm[wv] = v;
+  __syncthreads();
+  float r = shm[0];
+  for (int k = 1; k < NT / 64; k++) r += shm[k];
+  return r;
+}
+
+// Register-resident rows: each of NT threads holds NV4 float4 of the row; one read, one write.
+template <int NT, int NV4, typename TOut>
+__global__ __launch_bounds__(NT) void ce_rows_reg_kernel(
+    const float* __restrict__ logits, const int32_t* __restrict__ labels, TOut* __restrict__ dL,
+    float* __restrict__ row_loss, const int* __restrict__ count, int T, int V, int ignoreId,
+    float smoothing) {
+  __shared__ float shm[4 * NT / 64];
+  const int real = *count;
+  const float scale = real > 0 ? 1.f / (float)real : 0.f;
+  const float epsOverV = smoothing / (float)V, oneMinusE = 1.f - smoothing;
+  for (int t = blockIdx.x; t < T; t += gridDim.x) {
+    const int lab = labels[t];
+    const float* z = logits + (int64_t)t * V;
+    TOut* d = dL + (int64_t)t * V;
+    if (lab == ignoreId) {  // reference leaves ignored rows zero
+      for (int c = threadIdx.x; c < V; c += NT) d[c] = (TOut)0;
+      if (threadIdx.x == 0 && row_loss) row_loss[t] = 0.f;
+      continue;
+    }
+    float4 r[NV4];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NV4; j++) {
+      const int c = (j * NT + threadIdx.x) * 4;
+      if (c + 3 < V) {
+        r[j] = ld4(z + c);
+      } else {
+        r[j].x = c < V ? z[c] : -INFINITY;
+        r[j].y = c + 1 < V ? z[c + 1] : -INFINITY;
+        r[j].z = c + 2 < V ? z[c + 2] : -INFINITY;
+        r[j].w = c + 3 < V ? z[c + 3] : -INFINITY;
+      }
+      m = fmaxf(m, fmaxf(fmaxf(r[j].x, r[j].y), fmaxf(r[j].z, r[j].w)));
+    }
+    m = block_max<NT>(m, shm);
+    float sum = 0.f, zsum = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV4; j++) {
+      const int c = (j * NT + threadIdx.x) * 4;
+      if (c < V) zsum += r[j].x + (c + 1 < V ? r[j].y : 0.f) + (c + 2 < V ? r[j].z : 0.f) + (c + 3 < V ? r[j].w : 0.f);
+      r[j].x = expf(r[j].x - m);
+      r[j].y = expf(r[j].y - m);
+      r[j].z = expf(r[j].z - m);
+      r[j].w = expf(r[j].w - m);
+      sum += (r[j].x + r[j].y) + (r[j].z + r[j].w);
+    }
+    sum = block_sum<NT>(sum, shm + NT / 64);
+    if (smoothing > 0.f) zsum = block_sum<NT>(zsum, shm + NT / 64 + NT / 64);
+    const float inv = 1.f / sum;
+#pragma unroll
+    for (int j = 0; j < NV4; j++) {
+      const int c = (j * NT + threadIdx.x) * 4;
+      float e[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        if (c + v < V) {
+          float p = e[v] * inv;
+          if (smoothing > 0.f) {
+            p -= epsOverV;
+            if (c + v == lab) p -= oneMinusE;
+          } else if (c + v == lab) {
+            p -= 1.f;
+          }
+          e[v] = p * scale;
+        }
+      }
+      if constexpr (sizeof(TOut) == 4) {
+        if (c + 3 < V) {
+          st4((float*)(d + c), make_float4(e[0], e[1], e[2], e[3]));
+        } else {
+          for (int v = 0; v < 4; v++) if (c + v < V) d[c + v] = e[v];
+        }
+      } else {
+        for (int v = 0; v < 4; v++) if (c + v < V) store_out(d + c + v, e[v]);
+      }
+    }
+    if (threadIdx.x == 0 && row_loss) {
+      float lp = (z[lab] - m) - logf(sum);
+      if (smoothing <= 0.f) {
+        row_loss[t] = -lp;
+      } else {
+        float slp = zsum - (float)V * m - (float)V * logf(sum);
+        row_loss[t] = -(oneMinusE * lp + epsOverV * slp);
+      }
+    }
+  }
+}
+
+// Two-pass rows for any V: pass 1 online (max, sum-exp), pass 2 writes the gradient.
+template <int NT, typename TOut>
+__global__ __launch_bounds__(NT) void ce_rows_2pass_kernel(
+    const float* __restrict__ logits, const int32_t* __restrict__ labels, TOut* __restrict__ dL,
+    float* __restrict__ row_loss, const int* __restrict__ count, int T, int V, int ignoreId,
+    float smoothing) {
+  __shared__ float shm[2 * NT / 64 + 2 * NT / 64];
+  const int real = *count;
+  const float scale = real > 0 ? 1.f / (float)real : 0.f;
+  const float epsOverV = smoothing / (float)V, oneMinusE = 1.f - smoothing;
+  for (int t = blockIdx.x; t < T; t += gridDim.x) {
+    const int lab = labels[t];
+    const float* z = logits + (int64_t)t * V;
+    TOut* d = dL + (int64_t)t * V;
+    if (lab == ignoreId) {
+      for (int c = threadIdx.x; c < V; c += NT) d[c] = (TOut)0;
+      if (threadIdx.x == 0 && row_loss) row_loss[t] = 0.f;
+      continue;
+    }
+    float m = -INFINITY, s = 0.f, zsum = 0.f;
+    for (int c = threadIdx.x; c < V; c += NT) {
+      float v = z[c];
+      zsum += v;
+      if (v > m) { s = s * expf(m - v) + 1.f; m = v; }
+      else s += expf(v - m);
+    }
+    block_max_sum<NT>(m, s, shm);
+    if (smoothing > 0.f) zsum = block_sum<NT>(zsum, shm + 2 * NT / 64);
+    const float zl = z[lab];
+    __syncthreads();  // z may alias d
+    const float inv = 1.f / s;
+    for (int c = threadIdx.x; c < V; c += NT) {
+      float p = expf(z[c] - m) * inv;
+      if (smoothing > 0.f) {
+        p -= epsOverV;
+        if (c == lab) p -= oneMinusE;
+      } else if (c == lab) {
+        p -= 1.f;
+      }
+      store_out(d + c, p * scale);
+    }
+    if (threadIdx.x == 0 && row_loss) {
+      float lp = (zl - m) - logf(s);
+      if (smoothing <= 0.f) {
+        row_loss[t] = -lp;
+      } else {
+        float slp = zsum - (float)V * m - (float)V * logf(s);
+        row_loss[t] = -(oneMinusE * lp + epsOverV * slp);
+      }
+    }
+  }
+}
+
+__global__ void mean_loss_kernel(const float* __restrict__ row_loss, const int* __restrict__ count,
+                                 int T, float* __restrict__ out) {
+  __shared__ double sh[kBlock];
+  double a = 0.0;
+  for (int t = threadIdx.x; t < T; t += kBlock) a += (double)row_loss[t];
+  sh[threadIdx.x] = a;
+  __syncthreads();
+  for (int o = kBlock / 2; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) sh[threadIdx.x] += sh[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *out = *count > 0 ? (float)(sh[0] / *count) : 0.f;
+}
+
+template <typename TOut>
+static int ce_launch(const float* logits, const int32_t* labels, TOut* dL, float* loss, int T, int V,
+                     int ignoreId, float smoothing, hipStream_t s) {
+  if (T <= 0) return SMHIP_OK;
+  char* ws = (char*)workspace(s, 256 + sizeof(float) * (size_t)T, 1);
+  if (!ws) return fail(SMHIP_ENOMEM, "cross entropy: workspace");
+  int* count = (int*)ws;
+  float* row_loss = (float*)(ws + 256);
+  hipLaunchKernelGGL(count_labels_kernel, dim3(1), dim3(kBlock), 0, s, labels, T, ignoreId, count);
+  int G = grid_for(T, 1, 2);
+  const bool v4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dL % 16 == 0);
+  if (v4 && V <= 1024 * 4 * 8 && V > 256 * 4 * 8)
+    hipLaunchKernelGGL((ce_rows_reg_kernel<1024, 8, TOut>), dim3(G), dim3(1024), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
+  else if (v4 && V <= 256 * 4 * 8)
+    hipLaunchKernelGGL((ce_rows_reg_kernel<256, 8, TOut>), dim3(G), dim3(256), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
+  else
+    hipLaunchKernelGGL((ce_rows_2pass_kernel<1024, TOut>), dim3(G), dim3(1024), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
+  SMHIP_CHECK_LAUNCH();
+  if (loss) {
+    hipLaunchKernelGGL(mean_loss_kernel, dim3(1), dim3(kBlock), 0, s, row_loss, count, T, loss);
+    SMHIP_CHECK_LAUNCH();
+  }
+  return SMHIP_OK;
+}
+
+int ce_softmax_grad(const float* logits, const int32_t* labels, float* dL, float* loss, int T, int V,
+                    int ignoreId, float smoothing, hipStream_t s) {
+  return ce_launch<float>(logits, labels, dL, loss, T, V, ignoreId, smoothing, s);
+}
+int ce_softmax_grad_bf16(const float* logits, const int32_t* labels, uint16_t* dL, float* loss,
+                         int T, int V, int ignoreId, float smoothing, hipStream_t s) {
+  return ce_launch<uint16_t>(logits, labels, dL, loss, T, V, ignoreId, smoothing, s);
+}
+
+// ============================================================================
+// AdamW (TrainingKernels.cs:19-89): exact per-element IEEE op order of the reference
+// ============================================================================
+__device__ inline void adam_one(float& d, float g, float& m, float& v, float b1, float b2,
+                                float omb1, float omb2, float bc1, float bc2, float lr, float eps,
+                                float decay) {
+  m = b1 * m + omb1 * g;
+  v = b2 * v + omb2 * (g * g);
+  float mhat = m / bc1, vhat = v / bc2;
+  d = d - lr * (mhat / (sqrtf(vhat) + eps) + decay * d);
+}
+
+__global__ __launch_bounds__(kBlock) void adamw_kernel(float* __restrict__ data, const float* __restrict__ grad,
+                                                       float* __restrict__ m, float* __restrict__ v,
+                                                       int64_t n, float b1, float b2, float bc1,
+                                                       float bc2, float lr, float eps, float decay,
+                                                       int vec) {
+  const float omb1 = 1.f - b1, omb2 = 1.f - b2;
+  if (vec) {
+    const int64_t n4 = n / 4;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += (int64_t)gridDim.x * kBlock) {
+      float4 d = ld4(data + 4 * i), g = ld4(grad + 4 * i), mm = ld4(m + 4 * i), vv = ld4(v + 4 * i);
+      adam_one(d.x, g.x, mm.x, vv.x, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
+      adam_one(d.y, g.y, mm.y, vv.y, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
+      adam_one(d.z, g.z, mm.z, vv.z, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
+      adam_one(d.w, g.w, mm.w, vv.w, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
+      st4(m + 4 * i, mm);
+      st4(v + 4 * i, vv);
+      st4(data + 4 * i, d);
+    }
+    for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
+      adam_one(data[i], grad[i], m[i], v[i], b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
+  } else {
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
+      adam_one(data[i], grad[i], m[i], v[i], b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
+  }
+}
+
+int adamw_update(float* data, const float* grad, float* m, float* v, int64_t n, float b1, float b2,
+                 float bc1, float bc2, float lr, float eps, float decay, hipStream_t s) {
+  if (n <= 0) return SMHIP_OK;
+  int vec = ((uintptr_t)data | (uintptr_t)grad | (uintptr_t)m | (uintptr_t)v) % 16 == 0;
+  hipLaunchKernelGGL(adamw_kernel, dim3(grid_for(vec ? n / 4 + 1 : n, kBlock, 4)), dim3(kBlock), 0,
+                     s, data, grad, m, v, n, b1, b2, bc1, bc2, lr, eps, decay, vec);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// ============================================================================
+// L2 norm squared (TrainingKernels.cs:94-135): double partials per block, fixed-order final sum
+// ============================================================================
+__global__ __launch_bounds__(kBlock) void l2_partial_kernel(const float* __restrict__ x, int64_t n,
+                                                            double* __restrict__ part) {
+  __shared__ double sh[kBlock / 64];
+  double a = 0.0;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock) {
+    float v = x[i];
+    a += (double)(v * v);
+  }
+  a = wave_sum_d(a);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = a;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double r = 0.0;
+    for (int k = 0; k < kBlock / 64; k++) r += sh[k];
+    part[blockIdx.x] = r;
+  }
+}
+__global__ void l2_final_kernel(const double* __restrict__ part, int G, float* __restrict__ out,
+                                int accumulate) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    double r = 0.0;
+    for (int g = 0; g < G; g++) r += part[g];
+    *out = accumulate ? (float)((double)*out + r) : (float)r;
+  }
+}
+
+int l2normsq(const float* x, int64_t n, float* out, int accumulate, hipStream_t s) {
+  int G = grid_for(n > 0 ? n : 1, kBlock, 4);
+  double* part = (double*)workspace(s, sizeof(double) * G, 2);
+  if (!part) return fail(SMHIP_ENOMEM, "l2normsq: workspace");
+  hipLaunchKernelGGL(l2_partial_kernel, dim3(G), dim3(kBlock), 0, s, x, n, part);
+  hipLaunchKernelGGL(l2_final_kernel, dim3(1), dim3(64), 0, s, part, G, out, accumulate);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+__global__ void scale_kernel(float* __restrict__ x, int64_t n, float sc) {
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
+    x[i] *= sc;
+}
+int scale_inplace(float* x, int64_t n, float sc, hipStream_t s) {
+  if (n <= 0) return SMHIP_OK;
+  hipLaunchKernelGGL(scale_kernel, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, x, n, sc);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// ============================================================================
+// Embedding backward (GradientKernels.Embedding_Scalar, GradientKernels.cs:490-506)
+// Deterministic and bit-identical to the reference: the block owning the first
+// occurrence of an id adds every occurrence's row into dE[id] in token order.
+// ============================================================================
+__global__ __launch_bounds__(kBlock) void embedding_bwd_kernel(const float* __restrict__ dY,
+                                                               const int32_t* __restrict__ ids,
+                                                               float* __restrict__ dE, int T,
+                                                               int D, int V) {
+  __shared__ int dup;
+  for (int t = blockIdx.x; t < T; t += gridDim.x) {
+    const int id = ids[t];
+    if (threadIdx.x == 0) dup = 0;
+    __syncthreads();
+    for (int u = threadIdx.x; u < t; u += kBlock)
+      if (ids[u] == id) dup = 1;
+    __syncthreads();
+    const int is_dup = dup;
+    __syncthreads();
+    if (is_dup || id < 0 || id >= V) continue;
+    for (int d = threadIdx.x; d < D; d += kBlock) {
+      float acc = dE[(int64_t)id * D + d];
+      for (int u = t; u < T; u++)
+        if (ids[u] == id) acc = acc + dY[(int64_t)u * D + d];
+      dE[(int64_t)id * D + d] = acc;
+    }
+  }
+}
+
+int embedding_backward(const float* dY, const int32_t* ids, float* dE, int T, int D, int V,
+                       hipStream_t s) {
+  if (T <= 0) return SMHIP_OK;
+  hipLaunchKernelGGL(embedding_bwd_kernel, dim3(grid_for(T, 1, 8)), dim3(kBlock), 0, s, dY, ids,
+                     dE, T, D, V);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// Embedding forward gather: out[t] = E[ids[t]] (EmbeddingTable.cs:87)
+__global__ __launch_bounds__(kBlock) void embedding_fwd_kernel(const float* __restrict__ E,
+                                                               const int32_t* __restrict__ ids,
+                                                               float* __restrict__ out, int T, int D) {
+  for (int t = blockIdx.x; t < T; t += gridDim.x)
+    for (int d = threadIdx.x; d < D; d += kBlock) out[(int64_t)t * D + d] = E[(int64_t)ids[t] * D + d];
+}
+int embedding_forward(const float* E, const int32_t* ids, float* out, int T, int D, hipStream_t s) {
+  hipLaunchKernelGGL(embedding_fwd_kernel, dim3(grid_for(T, 1, 8)), dim3(kBlock), 0, s, E, ids, out, T, D);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// ============================================================================
+// small helpers for the engine / slot wrappers
+// ============================================================================
+__global__ void add_kernel(float* __restrict__ y, const float* __restrict__ x, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
+    y[i] = y[i] + x[i];
+}
+int add_inplace(float* y, const float* x, int64_t n, hipStream_t s) {
+  if (n <= 0) return SMHIP_OK;
+  hipLaunchKernelGGL(add_kernel, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, y, x, n);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+__global__ void f32_to_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
+    y[i] = f2bf(x[i]);
+}
+int f32_to_bf16(const float* x, uint16_t* y, int64_t n, hipStream_t s) {
+  if (n <= 0) return SMHIP_OK;
+  hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, x, y, n);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// Column sums (bias gradient, GradientKernels.cs:100-109): db[o] += sum_b dY[b,o], b ascending.
+__global__ void colsum_add_kernel(const float* __restrict__ dY, float* __restrict__ db, int B, int Out) {
+  int o = blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= Out) return;
+  float acc = 0.f;
+  for (int b = 0; b < B; b++) acc += dY[(int64_t)b * Out + o];
+  db[o] += acc;
+}
+int colsum_add(const float* dY, float* db, int B, int Out, hipStream_t s) {
+  if (Out <= 0) return SMHIP_OK;
+  hipLaunchKernelGGL(colsum_add_kernel, dim3(ceil_div(Out, 256)), dim3(256), 0, s, dY, db, B, Out);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+}  // namespace smhip

@@ -1,0 +1,52 @@
+// kernels.hpp — internal launchers shared between translation units.
+#pragma once
+#include "common.hpp"
+
+namespace smhip {
+
+// elementwise.hip
+int rmsnorm_backward(const float* dY, const float* xin, int from_x, const float* rinv,
+                     const float* w, float* dw, float* dX, int T, int D, int accumulate,
+                     uint16_t* dX_bf16, hipStream_t s);
+int rmsnorm_forward(const float* x, const float* w, float* y, uint16_t* yb, float* rinv, int T,
+                    int D, float eps, hipStream_t s);
+int layernorm_backward(const float* dY, const float* x, const float* w, float* dw, float* db,
+                       float* dX, int T, int D, float eps, hipStream_t s);
+int swiglu_backward_f32(const float* dAct, const float* gate, const float* up, float* dFused, int T,
+                        int F, hipStream_t s);
+int swiglu_backward_mixed(const float* dAct, const uint16_t* gu, uint16_t* dgu, int T, int F,
+                          hipStream_t s);
+int swiglu_forward_f32(const float* g, const float* u, float* a, int64_t n, hipStream_t s);
+int swiglu_forward_bf16(const uint16_t* gu, uint16_t* act, int T, int F, hipStream_t s);
+int silu_backward(const float* dy, const float* x, float* dx, int64_t n, hipStream_t s);
+int gelu_backward(const float* dy, const float* x, float* dx, int64_t n, hipStream_t s);
+int rope_apply(float* x, const float* cosT, const float* sinT, int B, int S, int H, int D, int neox,
+               int backward, hipStream_t s);
+int ce_softmax_grad(const float* logits, const int32_t* labels, float* dL, float* loss, int T, int V,
+                    int ignoreId, float smoothing, hipStream_t s);
+int ce_softmax_grad_bf16(const float* logits, const int32_t* labels, uint16_t* dL, float* loss,
+                         int T, int V, int ignoreId, float smoothing, hipStream_t s);
+int adamw_update(float* data, const float* grad, float* m, float* v, int64_t n, float b1, float b2,
+                 float bc1, float bc2, float lr, float eps, float decay, hipStream_t s);
+int l2normsq(const float* x, int64_t n, float* out, int accumulate, hipStream_t s);
+int scale_inplace(float* x, int64_t n, float sc, hipStream_t s);
+int embedding_backward(const float* dY, const int32_t* ids, float* dE, int T, int D, int V,
+                       hipStream_t s);
+int embedding_forward(const float* E, const int32_t* ids, float* out, int T, int D, hipStream_t s);
+int add_inplace(float* y, const float* x, int64_t n, hipStream_t s);
+int f32_to_bf16(const float* x, uint16_t* y, int64_t n, hipStream_t s);
+int colsum_add(const float* dY, float* db, int B, int Out, hipStream_t s);
+
+// quant.hip
+int dequant_raw(int qtype, const void* raw, float* out, int64_t n, hipStream_t s);
+size_t planes_bytes(int qtype, int64_t n, size_t* qs_bytes);
+int repack_planes(int qtype, const void* raw, int64_t n, void* dst, QuantPlanes* out, hipStream_t s);
+
+// attention.hip
+int attention_slot_backward(const float* dO, const float* q, const float* k, const float* v,
+                            const float* P, float* dQ, float* dK, float* dV, int S, int D,
+                            float scale, hipStream_t s);
+int attention_forward_probs(const float* q, const float* k, const float* v, float* probs, float* out,
+                            int B, int S, int Hq, int Hkv, int D, hipStream_t s);
+
+}  // namespace smhip

@@ -1,0 +1,138 @@
+// quant.hip — Q8_0 / Q4_K handling for gfx950.
+//
+// Reference byte layouts (QuantizationOps.cs:37; QuantizationKernels.Q4.cs:586-624):
+//   Q8_0 block  = 34 B : fp16 d @0, 32 x int8 @2; value = q * d.
+//   Q4_K block  = 144 B: fp16 d @0, fp16 dmin @2, 12 B packed 6-bit scales/mins @4,
+//                        128 B nibbles @16; value = (sc*v)*d - mn*dmin.
+// Both formats are flat streams of blocks over the row-major [rows][K] matrix.
+//
+// The 34-byte Q8_0 block is not 4-byte aligned, which defeats wide loads, so
+// weights that stay resident on the GPU are repacked ONCE into planes with
+// exactly the same bits: an int8 (or nibble) value plane with 16-byte aligned
+// rows, plus an fp32 scale plane.  fp32 scales are exact (every binary16 value
+// is representable) and, for Q4_K, sc*d and mn*dmin are exact products
+// (6-bit x 11-bit mantissas), so dequantising from the planes yields the same
+// fp32 values bit for bit as the reference's ReadQ8_0_Scalar / ReadQ4K_Scalar.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace smhip {
+
+__device__ inline uint16_t rd_u16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+__device__ inline int k4_scale(int j, const uint8_t* s) {
+  return j < 4 ? (s[j] & 0x3F) : ((s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4));
+}
+__device__ inline int k4_min(int j, const uint8_t* s) {
+  return j < 4 ? (s[j + 4] & 0x3F) : ((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+}
+
+// ---------------------------------------------------------------- direct dequant (bit-exact)
+__global__ void dequant_q8_0_kernel(const uint8_t* __restrict__ raw, float* __restrict__ out, int64_t n) {
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const uint8_t* blk = raw + (e >> 5) * 34;
+    float d = half_bits_to_float(rd_u16(blk));
+    out[e] = (float)(int8_t)blk[2 + (e & 31)] * d;
+  }
+}
+
+__global__ void dequant_q4k_kernel(const uint8_t* __restrict__ raw, float* __restrict__ out, int64_t n) {
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const uint8_t* blk = raw + (e >> 8) * 144;
+    const int i = (int)(e & 255);
+    float dS = half_bits_to_float(rd_u16(blk)), mS = half_bits_to_float(rd_u16(blk + 2));
+    float s = (float)k4_scale(i >> 5, blk + 4), m = (float)k4_min(i >> 5, blk + 4);
+    int v = (blk[16 + (i >> 6) * 32 + (i & 31)] >> (((i & 63) >> 5) * 4)) & 0x0F;
+    float t1 = s * (float)v;
+    t1 = t1 * dS;
+    out[e] = t1 - m * mS;
+  }
+}
+
+int dequant_raw(int qtype, const void* raw, float* out, int64_t n, hipStream_t s) {
+  if (n <= 0) return SMHIP_OK;
+  int g = (int)std::min<int64_t>((n + 255) / 256, (int64_t)num_cus() * 16);
+  if (qtype == SMHIP_QTYPE_Q8_0)
+    hipLaunchKernelGGL(dequant_q8_0_kernel, dim3(g), dim3(256), 0, s, (const uint8_t*)raw, out, n);
+  else if (qtype == SMHIP_QTYPE_Q4_K)
+    hipLaunchKernelGGL(dequant_q4k_kernel, dim3(g), dim3(256), 0, s, (const uint8_t*)raw, out, n);
+  else
+    return fail(SMHIP_EUNSUPPORTED, "dequant: qtype must be Q8_0 (8) or Q4_K (12)");
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// ---------------------------------------------------------------- repack to planes
+// Q8_0: one thread per 32-element block; qs plane int8[n], d plane f32[n/32].
+__global__ void repack_q8_0_kernel(const uint8_t* __restrict__ raw, int8_t* __restrict__ qs,
+                                   float* __restrict__ d, int64_t nblocks) {
+  for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblocks; b += (int64_t)gridDim.x * blockDim.x) {
+    const uint8_t* blk = raw + b * 34;
+    d[b] = half_bits_to_float(rd_u16(blk));
+    uint32_t w[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      w[j] = (uint32_t)blk[2 + 4 * j] | ((uint32_t)blk[3 + 4 * j] << 8) | ((uint32_t)blk[4 + 4 * j] << 16) |
+             ((uint32_t)blk[5 + 4 * j] << 24);
+    uint4* dst = reinterpret_cast<uint4*>(qs + b * 32);
+    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+  }
+}
+
+// Q4_K: one thread per 256-element super-block; qs plane = the 128 nibble bytes,
+// sm plane = 8 x (sc*d, mn*dmin) float pairs.
+__global__ void repack_q4k_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ qs,
+                                  float* __restrict__ sm, int64_t nblocks) {
+  for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblocks; b += (int64_t)gridDim.x * blockDim.x) {
+    const uint8_t* blk = raw + b * 144;
+    float dS = half_bits_to_float(rd_u16(blk)), mS = half_bits_to_float(rd_u16(blk + 2));
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      sm[b * 16 + 2 * j] = (float)k4_scale(j, blk + 4) * dS;
+      sm[b * 16 + 2 * j + 1] = (float)k4_min(j, blk + 4) * mS;
+    }
+    for (int j = 0; j < 128; j += 4) {
+      uint32_t w = (uint32_t)blk[16 + j] | ((uint32_t)blk[17 + j] << 8) | ((uint32_t)blk[18 + j] << 16) |
+                   ((uint32_t)blk[19 + j] << 24);
+      *reinterpret_cast<uint32_t*>(qs + b * 128 + j) = w;
+    }
+  }
+}
+
+size_t planes_bytes(int qtype, int64_t n, size_t* qs_bytes) {
+  size_t q = 0, sc = 0;
+  if (qtype == SMHIP_QTYPE_Q8_0) { q = (size_t)n; sc = sizeof(float) * (size_t)(n / 32); }
+  else if (qtype == SMHIP_QTYPE_Q4_K) { q = (size_t)n / 2; sc = sizeof(float) * 2 * (size_t)(n / 32); }
+  q = (q + 255) & ~(size_t)255;
+  if (qs_bytes) *qs_bytes = q;
+  return q + sc;
+}
+
+int repack_planes(int qtype, const void* raw, int64_t n, void* dst, QuantPlanes* out, hipStream_t s) {
+  size_t qb = 0;
+  planes_bytes(qtype, n, &qb);
+  out->kind = qtype;
+  out->n = n;
+  out->qs = dst;
+  out->sc = (float*)((char*)dst + qb);
+  if (qtype == SMHIP_QTYPE_Q8_0) {
+    SMHIP_REQUIRE(n % 32 == 0, "Q8_0 repack: element count must be a multiple of 32");
+    int64_t nb = n / 32;
+    int g = (int)std::min<int64_t>((nb + 255) / 256, (int64_t)num_cus() * 8);
+    hipLaunchKernelGGL(repack_q8_0_kernel, dim3(g), dim3(256), 0, s, (const uint8_t*)raw,
+                       (int8_t*)out->qs, out->sc, nb);
+  } else if (qtype == SMHIP_QTYPE_Q4_K) {
+    SMHIP_REQUIRE(n % 256 == 0, "Q4_K repack: element count must be a multiple of 256");
+    int64_t nb = n / 256;
+    int g = (int)std::min<int64_t>((nb + 255) / 256, (int64_t)num_cus() * 8);
+    hipLaunchKernelGGL(repack_q4k_kernel, dim3(g), dim3(256), 0, s, (const uint8_t*)raw,
+                       (uint8_t*)out->qs, out->sc, nb);
+  } else {
+    return fail(SMHIP_EUNSUPPORTED, "repack: qtype must be Q8_0 (8) or Q4_K (12)");
+  }
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+}  // namespace smhip
