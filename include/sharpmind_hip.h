@@ -140,6 +140,76 @@ int smhip_attention_forward_probs(const float* q, const float* k, const float* v
                                   float* out, int B, int S, int Hq, int Hkv, int D,
                                   smhip_stream_t stream);
 
+/* Causal GQA attention on bf16 MFMA without materialised probabilities (the engine's
+ * bf16 path; mathematically the forward of BackpropEngine.cs:237-388 and the backward of
+ * GradientKernels.cs:408-481).  Row r = b*S + s of q holds head h at columns [h*D, h*D+D)
+ * (row stride ldq elements); likewise k/v with Hkv heads.  q/k/v/o/dO are bf16 (uint16
+ * bits), lse [B,Hq,S] fp32 in log2 units, dq/dk/dv fp32 (overwritten).  S % 128 == 0,
+ * D in {64, 128}.  Backward is deterministic (no atomics). */
+int smhip_flash_attention_forward(const void* q, const void* k, const void* v, void* o, float* lse,
+                                  int B, int S, int Hq, int Hkv, int D, int64_t ldq, int64_t ldk,
+                                  int64_t ldv, int64_t ldo, smhip_stream_t stream);
+int smhip_flash_attention_backward(const void* q, const void* k, const void* v, const void* o,
+                                   const void* dO, const float* lse, float* dq, float* dk, float* dv,
+                                   int B, int S, int Hq, int Hkv, int D, int64_t ldq, int64_t ldk,
+                                   int64_t ldv, int64_t ldo, int64_t lddo, int64_t lddq,
+                                   int64_t lddk, int64_t lddv, smhip_stream_t stream);
+
+/* TensorQuantizer.Quantize for Q8_0 / Q4_K on the device (TensorQuantizer.cs:80-144,
+ * TensorQuantizer.KQuant.cs:173-225): same bytes as the reference encoder. */
+int smhip_quantize(int qtype, const float* x, int64_t n, void* out, smhip_stream_t stream);
+
+/* ---------------------------------------------------------------- training engine
+ * One resident fwd+bwd+optimizer step of a decoder (TrainLoop.ForwardBackward +
+ * BackpropEngine + Gradients.ClipGlobalNorm + AdamW.Update; TrainLoop.cs:100-135,222-243).
+ * Tensor names: "emb", "norm_f", "l<i>.norm1|norm2|q_norm|k_norm", full-parameter
+ * "l<i>.wqkv|wo|wgu|wd" ([Out][In] fp32) and "l<i>.bqkv|bo|bgu|bd", LoRA
+ * "l<i>.lora.<q|k|v|o|gate|up|down>.<A|B>" (A [In,r], B [r,Out] fp32).  In LoRA mode
+ * "emb" and "l<i>.w*" take the reference's raw Q8_0 / Q4_K bytes. */
+typedef struct {
+  int n_layers, d_model, n_heads, n_kv_heads, head_dim, ffn_dim, vocab;
+  int batch, seq;
+  float norm_eps, rope_theta;
+  int rope_neox, qk_norm;
+  int base_qtype;       /* SMHIP_QTYPE_F32: full-parameter training; Q8_0 / Q4_K: frozen LoRA base */
+  int lora_rank;
+  float lora_alpha;
+  int precision;        /* SMHIP_PREC_FP32 | SMHIP_PREC_BF16 */
+  int use_bias;
+  float lr, beta1, beta2, adam_eps, weight_decay; /* AdamW (Optimizers/AdamW.cs:22-41) */
+  float max_grad_norm;  /* <= 0: no clipping (TrainConfig.GradClipNorm, TrainConfig.cs:20) */
+} smhip_model_config;
+
+int smhip_engine_create(const smhip_model_config* cfg, void** engine);
+int smhip_engine_destroy(void* engine);
+int smhip_engine_param_count(void* engine, int64_t* trainable, int64_t* frozen);
+int smhip_engine_set_tensor(void* engine, const char* name, const void* host, int64_t nbytes);
+/* which = 0: parameter, 1: gradient */
+int smhip_engine_get_tensor(void* engine, const char* name, int which, void* host, int64_t nbytes);
+/* Synthetic initialisation on the device: N(0,0.02) weights (quantised in LoRA mode), norms 1,
+ * biases 0, LoRA A Kaiming-uniform, B ~ N(0,1e-3). */
+int smhip_engine_init_synthetic(void* engine, uint64_t seed);
+/* ids/labels: device int32 [batch*seq] (label -100 = ignored); loss: device float or NULL. */
+int smhip_engine_forward_backward(void* engine, const int32_t* ids, const int32_t* labels, float* loss,
+                                  smhip_stream_t stream);
+/* Clip (if configured) + AdamW; grad_norm_sq: device float or NULL (pre-clip sum of squares). */
+int smhip_engine_optimizer_step(void* engine, float* grad_norm_sq, smhip_stream_t stream);
+int smhip_engine_step(void* engine, const int32_t* ids, const int32_t* labels, float* loss,
+                      smhip_stream_t stream);
+/* Diagnostics: copy a saved activation of the last forward to host memory.  what: "h_in", "h_mid",
+ * "xn1", "qkv", "q", "k", "v", "o", "gu", "act" (of `layer`), "h_fin", "logits" ("logits" holds
+ * dLogits after a fp32-mode backward).  Element type is bf16 for "xn1|q|k|v|o|gu|act" in bf16
+ * mode, fp32 otherwise. */
+int smhip_engine_read_activation(void* engine, const char* what, int layer, void* host, int64_t nbytes);
+/* Live kernel timing on the calling thread: between begin and end, the GEMM and flash-attention
+ * launchers bracket their kernels with HIP events on the launch stream.  end synchronises and writes
+ * out[3*c + {0,1,2}] = (milliseconds, launches, algorithmic flops) for category c
+ * (0 = MFMA GEMM kernel, 1 = flash forward, 2 = flash backward kernels), c < ncat. */
+int smhip_profile_begin(int max_events);
+int smhip_profile_end(double* out, int ncat);
+/* Uniform random token ids in [0, vocab) (synthetic batches). */
+int smhip_fill_token_ids(int32_t* ids, int64_t n, uint64_t seed, int vocab, smhip_stream_t stream);
+
 /* ---------------------------------------------------------------- host-pointer slot entries
  * Same semantics as the device entries above, on host memory (synchronous).  These are
  * what SharpMind.HIP's [PuzzlePeice] methods P/Invoke. */

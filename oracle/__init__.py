@@ -137,3 +137,51 @@ class DotNetRandom:
 
 def f32(a):
     return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---------------------------------------------------------------- engine (oracle/engine.c)
+class EngineCfg(ctypes.Structure):
+    _fields_ = [("L", c_int), ("d", c_int), ("Hq", c_int), ("Hkv", c_int), ("D", c_int), ("F", c_int),
+                ("V", c_int), ("B", c_int), ("S", c_int), ("eps", c_float), ("theta", c_float),
+                ("neox", c_int), ("qk_norm", c_int), ("lora_rank", c_int), ("lora_alpha", c_float)]
+
+
+PER_LAYER = ["norm1", "wqkv", "bqkv", "q_norm", "k_norm", "wo", "bo", "norm2", "wgu", "bgu", "wd", "bd"] + \
+    [f"lora.{p}.{m}" for p in ("q", "k", "v", "o", "gate", "up", "down") for m in ("A", "B")]
+
+
+def engine_index(name):
+    """Tensor index used by orc_engine_step: 0 emb, 1 norm_f, then 26 per layer."""
+    if name == "emb":
+        return 0
+    if name == "norm_f":
+        return 1
+    layer, rest = name.split(".", 1)
+    return 2 + int(layer[1:]) * len(PER_LAYER) + PER_LAYER.index(rest)
+
+
+def engine_step(cfg, params, grads, ids, labels, want_logits=False):
+    """Run orc_engine_step.  params/grads: dict name -> float32 ndarray (grads accumulate in place)."""
+    L = lib()
+    if not hasattr(L, "_engine_declared"):
+        L.orc_engine_step.restype = c_int
+        L.orc_engine_step.argtypes = [ctypes.POINTER(EngineCfg), ctypes.POINTER(ctypes.c_void_p),
+                                      ctypes.POINTER(ctypes.c_void_p), I32P, I32P,
+                                      ctypes.POINTER(c_float), ctypes.c_void_p]
+        L._engine_declared = True
+    n = 2 + cfg.L * len(PER_LAYER)
+    P = (ctypes.c_void_p * n)()
+    G = (ctypes.c_void_p * n)()
+    for k, a in params.items():
+        assert a.dtype == np.float32 and a.flags.c_contiguous
+        P[engine_index(k)] = a.ctypes.data
+    for k, a in grads.items():
+        assert a.dtype == np.float32 and a.flags.c_contiguous
+        G[engine_index(k)] = a.ctypes.data
+    loss = c_float(0)
+    logits = np.zeros((cfg.B * cfg.S, cfg.V), np.float32) if want_logits else None
+    rc = L.orc_engine_step(ctypes.byref(cfg), P, G, np.ascontiguousarray(ids, np.int32),
+                           np.ascontiguousarray(labels, np.int32), ctypes.byref(loss),
+                           logits.ctypes.data if want_logits else None)
+    assert rc == 0
+    return (loss.value, logits) if want_logits else loss.value

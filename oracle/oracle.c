@@ -368,7 +368,7 @@ void orc_grad_linear(const float* dY, const float* X, const float* W, float* dW,
       float* d = dX + (int64_t)b * In;
       for (int i = 0; i < In; i++) d[i] += g * w[i];
     }
-  for (int o = 0; o < Out; o++) {
+  for (int o = 0; o < Out && dW; o++) {
     float* dw = dW + (int64_t)o * In;
     for (int b = 0; b < B; b++) {
       float g = dY[(int64_t)b * Out + o];

@@ -11,7 +11,7 @@ import re
 HEADER = os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "include", "sharpmind_hip.h")
 
 _SCALARS = {
-    "int": ctypes.c_int, "int32_t": ctypes.c_int32, "int64_t": ctypes.c_int64,
+    "int": ctypes.c_int, "int32_t": ctypes.c_int32, "int64_t": ctypes.c_int64, "uint64_t": ctypes.c_uint64,
     "float": ctypes.c_float, "double": ctypes.c_double, "size_t": ctypes.c_size_t,
     "smhip_stream_t": ctypes.c_void_p, "void": None,
 }

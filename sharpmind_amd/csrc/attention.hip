@@ -123,3 +123,64 @@ int attention_forward_probs(const float* q, const float* k, const float* v, floa
 }
 
 }  // namespace smhip
+
+namespace smhip {
+
+// Head-strided form of the slot backward for the exactness engine: q/dq [B*S, Hq*D],
+// k/v/dk/dv [B*S, Hkv*D], probs [B, Hq, S, S].  dK/dV of query heads sharing a kv
+// head are summed in head order (BackpropEngine.cs:563-582 AddHead order).
+int attention_probs_backward(const float* dO, const float* q, const float* k, const float* v,
+                             const float* probs, float* dq, float* dk, float* dv, int B, int S, int Hq,
+                             int Hkv, int D, hipStream_t s) {
+  const int grp = Hq / Hkv;
+  const int64_t qd = (int64_t)Hq * D, kvd = (int64_t)Hkv * D;
+  float* dP = (float*)workspace(s, sizeof(float) * (size_t)S * S, 4);
+  if (!dP) return fail(SMHIP_ENOMEM, "attention backward: workspace");
+  int rz = zero_bytes(dk, sizeof(float) * (size_t)B * S * kvd, s);
+  if (!rz) rz = zero_bytes(dv, sizeof(float) * (size_t)B * S * kvd, s);
+  if (rz) return rz;
+  const float scale = 1.f / sqrtf((float)D);
+  for (int b = 0; b < B; b++)
+    for (int h = 0; h < Hq; h++) {
+      const int kvh = h / grp;
+      const float* P = probs + ((int64_t)b * Hq + h) * S * S;
+      const float* dOh = dO + (int64_t)b * S * qd + h * D;
+      const float* qh = q + (int64_t)b * S * qd + h * D;
+      const float* kh = k + (int64_t)b * S * kvd + kvh * D;
+      const float* vh = v + (int64_t)b * S * kvd + kvh * D;
+      GemmArgs g{};
+      g.precision = SMHIP_PREC_FP32;
+      g.split_k = 1;
+      g.alpha = 1.f;
+      // dV += P^T dO
+      g.M = S; g.N = D; g.K = S; g.beta = 1.f;
+      g.A = {SRC_F32_R, P, nullptr, S};
+      g.B = {SRC_F32_R, dOh, nullptr, qd};
+      g.C = dv + (int64_t)b * S * kvd + kvh * D; g.ldc = kvd;
+      int rc = gemm(g, s);
+      if (rc) return rc;
+      // dP = dO V^T
+      g.M = S; g.N = S; g.K = D; g.beta = 0.f;
+      g.A = {SRC_F32_K, dOh, nullptr, qd};
+      g.B = {SRC_F32_K, vh, nullptr, kvd};
+      g.C = dP; g.ldc = S;
+      if ((rc = gemm(g, s))) return rc;
+      hipLaunchKernelGGL(softmax_jacobian_rows, dim3(std::min(ceil_div(S, 4), num_cus() * 4)), dim3(256), 0, s, P, dP, S);
+      SMHIP_CHECK_LAUNCH();
+      // dQ = scale dS K
+      g.M = S; g.N = D; g.K = S; g.alpha = scale; g.beta = 0.f;
+      g.A = {SRC_F32_K, dP, nullptr, S};
+      g.B = {SRC_F32_R, kh, nullptr, kvd};
+      g.C = dq + (int64_t)b * S * qd + h * D; g.ldc = qd;
+      if ((rc = gemm(g, s))) return rc;
+      // dK += scale dS^T Q
+      g.beta = 1.f;
+      g.A = {SRC_F32_R, dP, nullptr, S};
+      g.B = {SRC_F32_R, qh, nullptr, qd};
+      g.C = dk + (int64_t)b * S * kvd + kvh * D; g.ldc = kvd;
+      if ((rc = gemm(g, s))) return rc;
+    }
+  return SMHIP_OK;
+}
+
+}  // namespace smhip

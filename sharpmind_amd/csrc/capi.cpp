@@ -64,9 +64,61 @@ void* workspace(hipStream_t s, size_t bytes, int slot) {
   return b.p;
 }
 
+struct Profiler {
+  std::vector<hipEvent_t> ev;
+  size_t used = 0;
+  struct Rec { int cat, i0, i1; double flops; };
+  std::vector<Rec> recs;
+};
+static thread_local Profiler* g_prof = nullptr;
+
+int prof_mark(hipStream_t s) {
+  Profiler* p = g_prof;
+  if (!p || p->used >= p->ev.size()) return -1;
+  hipEventRecord(p->ev[p->used], s);
+  return (int)p->used++;
+}
+void prof_add(int cat, int i0, int i1, double flops) {
+  if (g_prof && i0 >= 0 && i1 >= 0) g_prof->recs.push_back({cat, i0, i1, flops});
+}
+
 }  // namespace smhip
 
 using namespace smhip;
+
+extern "C" int smhip_profile_begin(int max_events) {
+  SMHIP_REQUIRE(max_events > 0, "profile_begin: max_events must be positive");
+  if (g_prof) return fail(SMHIP_EINVAL, "profile_begin: profiling already active on this thread");
+  Profiler* p = new Profiler();
+  p->ev.resize(max_events);
+  for (auto& e : p->ev) {
+    if (hipEventCreate(&e) != hipSuccess) { delete p; return fail(SMHIP_EHIP, "profile_begin: hipEventCreate"); }
+  }
+  g_prof = p;
+  return SMHIP_OK;
+}
+
+extern "C" int smhip_profile_end(double* out, int ncat) {
+  Profiler* p = g_prof;
+  SMHIP_REQUIRE(p, "profile_end: profiling not active");
+  g_prof = nullptr;
+  int rc = SMHIP_OK;
+  if (hipDeviceSynchronize() != hipSuccess) rc = fail(SMHIP_EHIP, "profile_end: synchronize failed");
+  if (!rc && out) {
+    for (int i = 0; i < 3 * ncat; i++) out[i] = 0.0;
+    for (auto& r : p->recs) {
+      if (r.cat >= ncat) continue;
+      float ms = 0.f;
+      hipEventElapsedTime(&ms, p->ev[r.i0], p->ev[r.i1]);
+      out[3 * r.cat] += ms;
+      out[3 * r.cat + 1] += 1.0;
+      out[3 * r.cat + 2] += r.flops;
+    }
+  }
+  for (auto& e : p->ev) hipEventDestroy(e);
+  delete p;
+  return rc;
+}
 
 #define STREAM(s) ((hipStream_t)(s))
 
@@ -452,6 +504,31 @@ int smhip_host_qmatmul(int qtype, const float* in, const void* rawW, float* out,
   if (a.sync()) return a.rc;
   a.down(out, p3, (size_t)M * N);
   return a.rc;
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int smhip_flash_attention_forward(const void* q, const void* k, const void* v, void* o, float* lse, int B, int S,
+                                  int Hq, int Hkv, int D, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
+                                  smhip_stream_t stream) {
+  SMHIP_REQUIRE(q && k && v && o && lse && B > 0 && S > 0, "flash_attention_forward: bad arguments");
+  return flash_forward((const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, B, S, Hq, Hkv,
+                       D, ldq, ldk, ldv, ldo, STREAM(stream));
+}
+
+int smhip_flash_attention_backward(const void* q, const void* k, const void* v, const void* o, const void* dO,
+                                   const float* lse, float* dq, float* dk, float* dv, int B, int S, int Hq, int Hkv,
+                                   int D, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, int64_t lddo,
+                                   int64_t lddq, int64_t lddk, int64_t lddv, smhip_stream_t stream) {
+  SMHIP_REQUIRE(q && k && v && o && dO && lse && dq && dk && dv && B > 0 && S > 0, "flash_attention_backward: bad arguments");
+  hipStream_t s = STREAM(stream);
+  void* ws = workspace(s, flash_backward_workspace(B, S, Hq, D), 6);
+  if (!ws) return fail(SMHIP_ENOMEM, "flash_attention_backward: workspace");
+  return flash_backward((const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)o,
+                        (const uint16_t*)dO, lse, dq, dk, dv, B, S, Hq, Hkv, D, ldq, ldk, ldv, ldo, lddo, lddq, lddk,
+                        lddv, ws, s);
 }
 
 }  // extern "C"

@@ -146,7 +146,17 @@ struct GemmArgs {
   int c_bf16;          // output stored as bf16
   int precision;       // SMHIP_PREC_FP32 | SMHIP_PREC_BF16
   int split_k;         // >1: deterministic split-K through workspace
+  const float* bias;   // optional per-column bias added in the epilogue
+  const float* R;      // optional residual: C = alpha*AB + bias + R  (fp32 output only)
+  int64_t ldr;
 };
 int gemm(const GemmArgs& g, hipStream_t s);
+
+// ---------------------------------------------------------------- live kernel timing
+// When enabled (smhip_profile_begin) the launchers bracket their main kernel with
+// HIP events on the launch stream; smhip_profile_end sums the elapsed times.
+enum ProfCat { PROF_GEMM = 0, PROF_FLASH_FWD = 1, PROF_FLASH_BWD = 2, PROF_NCAT = 3 };
+int prof_mark(hipStream_t s);                         // -1 when profiling is off
+void prof_add(int cat, int i0, int i1, double flops);
 
 }  // namespace smhip

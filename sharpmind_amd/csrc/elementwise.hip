@@ -559,6 +559,7 @@ __global__ __launch_bounds__(NT) void ce_rows_reg_kernel(
       if (threadIdx.x == 0 && row_loss) row_loss[t] = 0.f;
       continue;
     }
+    const float zl = threadIdx.x == 0 ? z[lab] : 0.f;  // read before the row is overwritten (dL may alias z)
     float4 r[NV4];
     float m = -INFINITY;
 #pragma unroll
@@ -617,7 +618,7 @@ __global__ __launch_bounds__(NT) void ce_rows_reg_kernel(
       }
     }
     if (threadIdx.x == 0 && row_loss) {
-      float lp = (z[lab] - m) - logf(sum);
+      float lp = (zl - m) - logf(sum);
       if (smoothing <= 0.f) {
         row_loss[t] = -lp;
       } else {

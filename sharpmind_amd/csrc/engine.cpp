@@ -1,0 +1,863 @@
+// engine.cpp — one training step of SharpMind's decoder on a single MI355X.
+//
+// Call order mirrors TrainLoop.ForwardBackward + BackpropEngine
+// (SharpMind.Training/TrainLoop.cs:222-243; Autograd/BackpropEngine.cs:73-206,
+// 517-657, 802-835) and then the optimizer (Gradients.ClipGlobalNorm,
+// Gradients.cs:92-116; AdamW.Update, Optimizers/AdamW.cs:52-89).  Everything
+// stays resident in HBM: weights, saved activations, gradients, AdamW state.
+// No allocation happens inside a step.
+//
+// Two modes share the code:
+//  * full-parameter (base_qtype = F32): every weight trains; precision fp32
+//    (fp32 MFMA, the exactness configuration) or bf16 (bf16 weight shadows
+//    with fp32 masters, bf16 MFMA);
+//  * LoRA (lora_rank > 0, base Q8_0 / Q4_K): the base is frozen and stored as
+//    repacked quantisation planes, dequantised in registers inside every GEMM;
+//    only the adapters train.  Fused projections (q|k|v, gate|up) carry one
+//    adapter of rank n*r whose B is block-diagonal; off-diagonal gradient
+//    blocks are zeroed so they stay exactly zero under AdamW.
+#include <hip/hip_runtime.h>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace smhip {
+
+enum Proj { P_QKV = 0, P_O = 1, P_GU = 2, P_D = 3 };
+
+struct DenseRef {  // trainable/frozen fp32 tensor inside an arena
+  float* data = nullptr;
+  float* grad = nullptr;  // null when frozen
+  uint16_t* bf = nullptr; // bf16 shadow (full-param bf16 mode, weights only)
+  int64_t n = 0;
+};
+
+struct LayerW {
+  DenseRef norm1, norm2, qn, kn;
+  DenseRef w[4], b[4];       // full-param weights [Out][In] and biases
+  QuantPlanes q[4];          // LoRA mode frozen base
+  void* qraw[4] = {};        // LoRA mode: planes storage
+  DenseRef la[4], lb[4];     // LoRA A [In, nr], B [nr, Out]
+  int* lb_cols = nullptr;    // device: column start of each diagonal block
+};
+
+struct Saved {
+  float *h_in, *rinv1, *qkv, *rinv_qk, *lse, *probs, *h_mid, *rinv2;
+  void *xn1, *q, *k, *v, *o, *xn2, *gu, *act;
+  void* u[4];  // LoRA x.A per projection
+};
+
+struct Engine {
+  smhip_model_config c;
+  int T, qd, kvd, nqkv, In[4], Out[4], nr[4], nblk[4];
+  bool bf, lora;
+  size_t esz;  // activation element size
+  // arenas
+  float* train = nullptr; float* grad = nullptr; float* m = nullptr; float* v = nullptr;
+  uint16_t* train_bf = nullptr;
+  int64_t n_train = 0, n_decay = 0;
+  float* frozen = nullptr;
+  int64_t n_frozen = 0;
+  std::vector<void*> allocs;
+  // tensors
+  DenseRef emb, norm_f;
+  QuantPlanes emb_q{};
+  std::vector<LayerW> L;
+  std::map<std::string, DenseRef*> dense_by_name;
+  // activations
+  std::vector<Saved> sv;
+  float *h_fin, *rinv_f, *logits, *cosT, *sinT, *loss, *gnorm;
+  void *xnf, *dlogits;
+  // backward work
+  float *dh, *dx, *dact, *dq, *dk, *dv;
+  void *dh_ta, *dgu, *dO, *dqkv, *z;
+  void* flash_ws = nullptr;
+  int step = 0;
+};
+
+static inline void* dalloc(Engine* e, size_t bytes) {
+  void* p = nullptr;
+  if (hipMalloc(&p, bytes < 256 ? 256 : bytes) != hipSuccess) return nullptr;
+  e->allocs.push_back(p);
+  return p;
+}
+
+static const char* kProjName[4] = {"qkv", "o", "gu", "d"};
+
+// ------------------------------------------------------------------ layout
+static int build(Engine* e) {
+  const smhip_model_config& c = e->c;
+  e->T = c.batch * c.seq;
+  e->qd = c.n_heads * c.head_dim;
+  e->kvd = c.n_kv_heads * c.head_dim;
+  e->nqkv = e->qd + 2 * e->kvd;
+  e->bf = c.precision == SMHIP_PREC_BF16;
+  e->lora = c.lora_rank > 0;
+  e->esz = e->bf ? 2 : 4;
+  const int d = c.d_model, F = c.ffn_dim, V = c.vocab, r = c.lora_rank;
+  e->In[P_QKV] = d; e->Out[P_QKV] = e->nqkv; e->nr[P_QKV] = 3 * r; e->nblk[P_QKV] = 3;
+  e->In[P_O] = e->qd; e->Out[P_O] = d; e->nr[P_O] = r; e->nblk[P_O] = 1;
+  e->In[P_GU] = d; e->Out[P_GU] = 2 * F; e->nr[P_GU] = 2 * r; e->nblk[P_GU] = 2;
+  e->In[P_D] = F; e->Out[P_D] = d; e->nr[P_D] = r; e->nblk[P_D] = 1;
+  e->L.resize(c.n_layers);
+
+  // --- arena sizing: trainable tensors, weight-decayed ones first (AdamW.cs:25-41 no-decay names)
+  struct Item { DenseRef* ref; int64_t n; bool decay; bool shadow; };
+  std::vector<Item> tr, fr;
+  auto add = [&](DenseRef* ref, int64_t n, bool trainable, bool decay, bool shadow) {
+    (trainable ? tr : fr).push_back({ref, n, decay, shadow});
+  };
+  const bool full = !e->lora;
+  add(&e->emb, (int64_t)V * d, full, true, true);  // LoRA mode keeps emb quantised (emb_q)
+  add(&e->norm_f, d, full, false, false);
+  for (int l = 0; l < c.n_layers; l++) {
+    LayerW& w = e->L[l];
+    add(&w.norm1, d, full, false, false);
+    add(&w.norm2, d, full, false, false);
+    if (c.qk_norm) { add(&w.qn, c.head_dim, full, false, false); add(&w.kn, c.head_dim, full, false, false); }
+    for (int p = 0; p < 4; p++) {
+      if (full) {
+        add(&w.w[p], (int64_t)e->Out[p] * e->In[p], true, true, true);
+        if (c.use_bias) add(&w.b[p], e->Out[p], true, false, false);
+      } else {
+        add(&w.la[p], (int64_t)e->In[p] * e->nr[p], true, true, false);
+        add(&w.lb[p], (int64_t)e->nr[p] * e->Out[p], true, true, false);
+      }
+    }
+  }
+  if (e->lora) {  // emb is frozen and quantised: not part of the fp32 arenas
+    for (size_t i = 0; i < fr.size(); i++)
+      if (fr[i].ref == &e->emb) { fr.erase(fr.begin() + i); break; }
+  }
+  std::stable_partition(tr.begin(), tr.end(), [](const Item& it) { return it.decay; });
+  for (auto& it : tr) { e->n_train += it.n; if (it.decay) e->n_decay += it.n; }
+  for (auto& it : fr) e->n_frozen += it.n;
+  const size_t tb = sizeof(float) * (size_t)std::max<int64_t>(e->n_train, 1);
+  e->train = (float*)dalloc(e, tb);
+  e->grad = (float*)dalloc(e, tb);
+  e->m = (float*)dalloc(e, tb);
+  e->v = (float*)dalloc(e, tb);
+  if (!e->train || !e->grad || !e->m || !e->v) return fail(SMHIP_ENOMEM, "engine: parameter arena");
+  if (full && e->bf) {
+    e->train_bf = (uint16_t*)dalloc(e, sizeof(uint16_t) * (size_t)std::max<int64_t>(e->n_train, 1));
+    if (!e->train_bf) return fail(SMHIP_ENOMEM, "engine: bf16 shadow");
+  }
+  if (e->n_frozen) {
+    e->frozen = (float*)dalloc(e, sizeof(float) * (size_t)e->n_frozen);
+    if (!e->frozen) return fail(SMHIP_ENOMEM, "engine: frozen arena");
+  }
+  // parameters start at zero (fused LoRA B off-diagonal blocks must stay exactly 0), AdamW m = v = 0
+  for (float* a : {e->train, e->grad, e->m, e->v})
+    if (int rc = zero_bytes(a, tb, nullptr)) return rc;
+  if (e->frozen)
+    if (int rc = zero_bytes(e->frozen, sizeof(float) * (size_t)e->n_frozen, nullptr)) return rc;
+  SMHIP_CHECK_HIP(hipDeviceSynchronize());
+  int64_t off = 0;
+  for (auto& it : tr) {
+    it.ref->data = e->train + off;
+    it.ref->grad = e->grad + off;
+    it.ref->bf = (e->train_bf && it.shadow) ? e->train_bf + off : nullptr;
+    it.ref->n = it.n;
+    off += it.n;
+  }
+  off = 0;
+  for (auto& it : fr) {
+    it.ref->data = e->frozen + off;
+    it.ref->grad = nullptr;
+    it.ref->n = it.n;
+    off += it.n;
+  }
+
+  // --- LoRA: quantised base planes and block-diagonal column starts
+  if (e->lora) {
+    const int qt = c.base_qtype;
+    SMHIP_REQUIRE(qt == SMHIP_QTYPE_Q8_0 || qt == SMHIP_QTYPE_Q4_K, "engine: LoRA base must be Q8_0 or Q4_K");
+    auto mk = [&](QuantPlanes* q, void** store, int64_t n) -> int {
+      size_t qb = 0;
+      size_t bytes = planes_bytes(qt, n, &qb);
+      *store = dalloc(e, bytes);
+      if (!*store) return fail(SMHIP_ENOMEM, "engine: quantised base");
+      q->kind = qt; q->n = n; q->qs = *store; q->sc = (float*)((char*)*store + qb);
+      return SMHIP_OK;
+    };
+    void* emb_store = nullptr;
+    if (int rc = mk(&e->emb_q, &emb_store, (int64_t)V * d)) return rc;
+    for (int l = 0; l < c.n_layers; l++)
+      for (int p = 0; p < 4; p++)
+        if (int rc = mk(&e->L[l].q[p], &e->L[l].qraw[p], (int64_t)e->Out[p] * e->In[p])) return rc;
+    for (int l = 0; l < c.n_layers; l++) {
+      // column start of each diagonal block of the fused B: q|k|v at [0..3), gate|up at [3..5)
+      LayerW& w = e->L[l];
+      w.lb_cols = (int*)dalloc(e, 8 * sizeof(int));
+      if (!w.lb_cols) return fail(SMHIP_ENOMEM, "engine: LoRA block table");
+      const int h_cols[5] = {0, e->qd, e->qd + e->kvd, 0, F};
+      SMHIP_CHECK_HIP(hipMemcpy(w.lb_cols, h_cols, sizeof(h_cols), hipMemcpyHostToDevice));
+    }
+  }
+
+  // --- activations
+  const int T = e->T;
+  const size_t ES = e->esz;
+  e->sv.resize(c.n_layers);
+  for (int l = 0; l < c.n_layers; l++) {
+    Saved& s = e->sv[l];
+    memset(&s, 0, sizeof(s));
+    s.h_in = (float*)dalloc(e, sizeof(float) * (size_t)T * d);
+    s.rinv1 = (float*)dalloc(e, sizeof(float) * T);
+    s.xn1 = dalloc(e, ES * (size_t)T * d);
+    s.qkv = (float*)dalloc(e, sizeof(float) * (size_t)T * e->nqkv);
+    s.rinv_qk = (float*)dalloc(e, sizeof(float) * (size_t)T * (c.n_heads + c.n_kv_heads));
+    s.q = dalloc(e, ES * (size_t)T * e->qd);
+    s.k = dalloc(e, ES * (size_t)T * e->kvd);
+    s.v = dalloc(e, ES * (size_t)T * e->kvd);
+    if (e->bf) s.lse = (float*)dalloc(e, sizeof(float) * (size_t)T * c.n_heads);
+    else s.probs = (float*)dalloc(e, sizeof(float) * (size_t)c.batch * c.n_heads * c.seq * c.seq);
+    s.o = dalloc(e, ES * (size_t)T * e->qd);
+    s.h_mid = (float*)dalloc(e, sizeof(float) * (size_t)T * d);
+    s.rinv2 = (float*)dalloc(e, sizeof(float) * T);
+    s.xn2 = dalloc(e, ES * (size_t)T * d);
+    s.gu = dalloc(e, ES * (size_t)T * 2 * F);
+    s.act = dalloc(e, ES * (size_t)T * F);
+    if (e->lora)
+      for (int p = 0; p < 4; p++) s.u[p] = dalloc(e, ES * (size_t)T * e->nr[p]);
+    if (!s.h_in || !s.act || !s.o || !s.gu) return fail(SMHIP_ENOMEM, "engine: activations");
+  }
+  e->h_fin = (float*)dalloc(e, sizeof(float) * (size_t)T * d);
+  e->rinv_f = (float*)dalloc(e, sizeof(float) * T);
+  e->xnf = dalloc(e, ES * (size_t)T * d);
+  e->logits = (float*)dalloc(e, sizeof(float) * (size_t)T * V);
+  e->dlogits = e->bf ? dalloc(e, 2 * (size_t)T * V) : (void*)e->logits;  // fp32 mode: in place
+  e->cosT = (float*)dalloc(e, sizeof(float) * (size_t)c.seq * c.head_dim / 2);
+  e->sinT = (float*)dalloc(e, sizeof(float) * (size_t)c.seq * c.head_dim / 2);
+  e->loss = (float*)dalloc(e, 256);
+  e->gnorm = e->loss + 4;
+  const int wmax = std::max(std::max(d, F), std::max(e->nqkv, 2 * F));
+  e->dh = (float*)dalloc(e, sizeof(float) * (size_t)T * d);
+  e->dx = (float*)dalloc(e, sizeof(float) * (size_t)T * d);
+  e->dact = (float*)dalloc(e, sizeof(float) * (size_t)T * F);
+  e->dq = (float*)dalloc(e, sizeof(float) * (size_t)T * e->qd);
+  e->dk = (float*)dalloc(e, sizeof(float) * (size_t)T * e->kvd);
+  e->dv = (float*)dalloc(e, sizeof(float) * (size_t)T * e->kvd);
+  e->dh_ta = e->bf ? dalloc(e, 2 * (size_t)T * d) : (void*)e->dh;
+  e->dgu = dalloc(e, ES * (size_t)T * 2 * F);
+  e->dO = dalloc(e, ES * (size_t)T * e->qd);
+  e->dqkv = dalloc(e, ES * (size_t)T * e->nqkv);
+  e->z = dalloc(e, ES * (size_t)T * std::max(3 * r, 1));
+  (void)wmax;
+  if (e->bf) e->flash_ws = dalloc(e, flash_backward_workspace(c.batch, c.seq, c.n_heads, c.head_dim));
+  if (!e->dh || !e->dgu || !e->dqkv || !e->logits || !e->dlogits || (e->bf && !e->flash_ws))
+    return fail(SMHIP_ENOMEM, "engine: work buffers");
+
+  // RoPE tables (host, RoPE.cs:99-148)
+  std::vector<float> ct((size_t)c.seq * c.head_dim / 2), st((size_t)c.seq * c.head_dim / 2);
+  if (int rc = smhip_rope_tables(c.rope_theta, c.head_dim, c.seq, ct.data(), st.data())) return rc;
+  SMHIP_CHECK_HIP(hipMemcpy(e->cosT, ct.data(), sizeof(float) * ct.size(), hipMemcpyHostToDevice));
+  SMHIP_CHECK_HIP(hipMemcpy(e->sinT, st.data(), sizeof(float) * st.size(), hipMemcpyHostToDevice));
+
+  // names
+  e->dense_by_name["emb"] = &e->emb;
+  e->dense_by_name["norm_f"] = &e->norm_f;
+  for (int l = 0; l < c.n_layers; l++) {
+    LayerW& w = e->L[l];
+    std::string p = "l" + std::to_string(l) + ".";
+    e->dense_by_name[p + "norm1"] = &w.norm1;
+    e->dense_by_name[p + "norm2"] = &w.norm2;
+    if (c.qk_norm) { e->dense_by_name[p + "q_norm"] = &w.qn; e->dense_by_name[p + "k_norm"] = &w.kn; }
+    if (!e->lora) {
+      const char* wn[4] = {"wqkv", "wo", "wgu", "wd"};
+      const char* bn[4] = {"bqkv", "bo", "bgu", "bd"};
+      for (int q = 0; q < 4; q++) {
+        e->dense_by_name[p + wn[q]] = &w.w[q];
+        if (c.use_bias) e->dense_by_name[p + bn[q]] = &w.b[q];
+      }
+    }
+  }
+  return SMHIP_OK;
+}
+
+// ------------------------------------------------------------------ operand helpers
+static Operand act_k(const Engine* e, const void* p, int64_t ld) {
+  return Operand{e->bf ? SRC_BF16_K : SRC_F32_K, p, nullptr, ld};
+}
+static Operand act_r(const Engine* e, const void* p, int64_t ld) {
+  return Operand{e->bf ? SRC_BF16_R : SRC_F32_R, p, nullptr, ld};
+}
+// weight W[Out][In] as the B operand of  y = x W^T (k = In contiguous)
+static Operand w_fwd(const Engine* e, const LayerW& w, int p) {
+  if (e->lora) {
+    const QuantPlanes& q = w.q[p];
+    return Operand{q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8_K : SRC_Q4K_K, q.qs, q.sc, e->In[p]};
+  }
+  return w.w[p].bf ? Operand{SRC_BF16_K, w.w[p].bf, nullptr, e->In[p]} : Operand{SRC_F32_K, w.w[p].data, nullptr, e->In[p]};
+}
+// weight as the B operand of  dX = dY W  (n = In, k = Out)
+static Operand w_bwd(const Engine* e, const LayerW& w, int p) {
+  if (e->lora) {
+    const QuantPlanes& q = w.q[p];
+    return Operand{q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8_R : SRC_Q4K_R, q.qs, q.sc, e->In[p]};
+  }
+  return w.w[p].bf ? Operand{SRC_BF16_R, w.w[p].bf, nullptr, e->In[p]} : Operand{SRC_F32_R, w.w[p].data, nullptr, e->In[p]};
+}
+static int prec(const Engine* e) { return e->bf ? SMHIP_PREC_BF16 : SMHIP_PREC_FP32; }
+static float lora_scale(const Engine* e) { return e->c.lora_alpha / (float)e->c.lora_rank; }
+
+static int split_for(int M, int N, int K) {
+  const int tiles = ceil_div(M, 128) * ceil_div(N, 128);
+  const int ks = ceil_div(K, 32);
+  if (tiles >= num_cus() || ks < 16) return 1;
+  int s = num_cus() / tiles;
+  s = std::min(s, ks / 4);
+  return std::max(1, std::min(s, 32));
+}
+
+// y (fp32 or TA) = x W^T [+ s (x A) B] [+ bias] [+ R]
+static int proj_forward(Engine* e, int l, int p, const void* x, void* y, int y_bf16, const float* R, hipStream_t s) {
+  LayerW& w = e->L[l];
+  const int T = e->T, In = e->In[p], Out = e->Out[p];
+  GemmArgs g{};
+  g.precision = prec(e);
+  g.alpha = 1.f;
+  g.split_k = 1;
+  if (e->lora) {  // u = x A  (saved for dB)
+    const int nr = e->nr[p];
+    GemmArgs u{};
+    u.precision = prec(e);
+    u.alpha = 1.f;
+    u.M = T; u.N = nr; u.K = In;
+    u.A = act_k(e, x, In);
+    u.B = Operand{SRC_F32_R, w.la[p].data, nullptr, nr};
+    u.C = e->sv[l].u[p]; u.ldc = nr; u.c_bf16 = e->bf;
+    u.split_k = split_for(T, nr, In);
+    if (int rc = gemm(u, s)) return rc;
+    g.K2 = nr;
+    g.A2 = act_k(e, e->sv[l].u[p], nr);
+    g.B2 = Operand{SRC_F32_R, w.lb[p].data, nullptr, Out};
+    g.alpha2 = lora_scale(e);
+  }
+  g.M = T; g.N = Out; g.K = In;
+  g.A = act_k(e, x, In);
+  g.B = w_fwd(e, w, p);
+  g.C = y; g.ldc = Out; g.c_bf16 = y_bf16;
+  g.bias = (!e->lora && e->c.use_bias) ? w.b[p].data : nullptr;
+  g.R = R; g.ldr = Out;
+  return gemm(g, s);
+}
+
+// dX (fp32 [T, In]) = dY W [+ s z A^T];  grads: dW += dY^T x (full), db, dA, dB (LoRA)
+static int proj_backward(Engine* e, int l, int p, const void* dY, const float* dY_f32, const void* x, float* dX,
+                         int dX_bf16, void* dX_out, hipStream_t s) {
+  LayerW& w = e->L[l];
+  const int T = e->T, In = e->In[p], Out = e->Out[p];
+  GemmArgs g{};
+  g.precision = prec(e);
+  g.alpha = 1.f;
+  g.split_k = 1;
+  if (e->lora) {
+    const int nr = e->nr[p];
+    const float sc = lora_scale(e);
+    // z = dY B^T   [T, nr]
+    GemmArgs z{};
+    z.precision = prec(e); z.alpha = 1.f;
+    z.M = T; z.N = nr; z.K = Out;
+    z.A = act_k(e, dY, Out);
+    z.B = Operand{SRC_F32_K, w.lb[p].data, nullptr, Out};
+    z.C = e->z; z.ldc = nr; z.c_bf16 = e->bf;
+    z.split_k = split_for(T, nr, Out);
+    if (int rc = gemm(z, s)) return rc;
+    // dB += s u^T dY   [nr, Out]
+    GemmArgs gb{};
+    gb.precision = prec(e); gb.alpha = sc; gb.beta = 1.f;
+    gb.M = nr; gb.N = Out; gb.K = T;
+    gb.A = act_r(e, e->sv[l].u[p], nr);
+    gb.B = act_r(e, dY, Out);
+    gb.C = w.lb[p].grad; gb.ldc = Out;
+    gb.split_k = split_for(nr, Out, T);
+    if (int rc = gemm(gb, s)) return rc;
+    if (e->nblk[p] > 1) {
+      if (p == P_QKV) {
+        if (int rc = lora_mask(w.lb[p].grad, nr, e->c.lora_rank, Out, w.lb_cols, 3, s)) return rc;
+      } else {
+        if (int rc = lora_mask(w.lb[p].grad, nr, e->c.lora_rank, Out, w.lb_cols + 3, 2, s)) return rc;
+      }
+    }
+    // dA += s x^T z   [In, nr]
+    GemmArgs ga{};
+    ga.precision = prec(e); ga.alpha = sc; ga.beta = 1.f;
+    ga.M = In; ga.N = nr; ga.K = T;
+    ga.A = act_r(e, x, In);
+    ga.B = act_r(e, e->z, nr);
+    ga.C = w.la[p].grad; ga.ldc = nr;
+    ga.split_k = split_for(In, nr, T);
+    if (int rc = gemm(ga, s)) return rc;
+    g.K2 = nr;
+    g.A2 = act_k(e, e->z, nr);
+    g.B2 = Operand{SRC_F32_K, w.la[p].data, nullptr, nr};
+    g.alpha2 = sc;
+  } else {
+    // dW += dY^T x   [Out, In]
+    GemmArgs gw{};
+    gw.precision = prec(e); gw.alpha = 1.f; gw.beta = 1.f;
+    gw.M = Out; gw.N = In; gw.K = T;
+    gw.A = act_r(e, dY, Out);
+    gw.B = act_r(e, x, In);
+    gw.C = w.w[p].grad; gw.ldc = In;
+    gw.split_k = split_for(Out, In, T);
+    if (int rc = gemm(gw, s)) return rc;
+    if (e->c.use_bias) {
+      SMHIP_REQUIRE(dY_f32, "engine: bias gradients need fp32 activations");
+      if (int rc = colsum_add(dY_f32, w.b[p].grad, T, Out, s)) return rc;
+    }
+  }
+  g.M = T; g.N = In; g.K = Out;
+  g.A = act_k(e, dY, Out);
+  g.B = w_bwd(e, w, p);
+  g.C = dX_out ? dX_out : (void*)dX; g.ldc = In; g.c_bf16 = dX_bf16;
+  return gemm(g, s);
+}
+
+// ------------------------------------------------------------------ step
+static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels, hipStream_t s) {
+  const smhip_model_config& c = e->c;
+  const int T = e->T, d = c.d_model, F = c.ffn_dim, V = c.vocab, Hq = c.n_heads, Hkv = c.n_kv_heads, D = c.head_dim;
+  int rc;
+#define R_(x) do { if ((rc = (x))) return rc; } while (0)
+  R_(zero_bytes(e->grad, sizeof(float) * (size_t)e->n_train, s));  // optimizer.ZeroGrad (TrainLoop.cs:109)
+
+  // ---------------- forward
+  if (e->lora) {
+    // embedding rows are gathered from the frozen quantised table: dequantise the needed rows
+    // (row t of E lives at flat elements ids[t]*d ...): gather via GEMM-free dequant path
+    R_(dequant_rows(e->emb_q, ids, e->sv[0].h_in, T, d, s));
+  } else {
+    R_(embedding_forward(e->emb.data, ids, e->sv[0].h_in, T, d, s));
+  }
+  for (int l = 0; l < c.n_layers; l++) {
+    Saved& sv = e->sv[l];
+    LayerW& w = e->L[l];
+    float* h_out = (l + 1 < c.n_layers) ? e->sv[l + 1].h_in : e->h_fin;
+    R_(rmsnorm_forward(sv.h_in, w.norm1.data, e->bf ? nullptr : (float*)sv.xn1, e->bf ? (uint16_t*)sv.xn1 : nullptr,
+                       sv.rinv1, T, d, c.norm_eps, s));
+    R_(proj_forward(e, l, P_QKV, sv.xn1, sv.qkv, 0, nullptr, s));
+    R_(qkv_prep_forward(sv.qkv, sv.q, sv.k, sv.v, sv.rinv_qk, c.qk_norm ? w.qn.data : nullptr,
+                        c.qk_norm ? w.kn.data : nullptr, e->cosT, e->sinT, T, c.seq, Hq, Hkv, D, c.qk_norm,
+                        c.rope_neox, c.norm_eps, e->bf, s));
+    if (e->bf) {
+      R_(flash_forward((const uint16_t*)sv.q, (const uint16_t*)sv.k, (const uint16_t*)sv.v, (uint16_t*)sv.o, sv.lse,
+                       c.batch, c.seq, Hq, Hkv, D, e->qd, e->kvd, e->kvd, e->qd, s));
+    } else {
+      R_(attention_forward_probs((const float*)sv.q, (const float*)sv.k, (const float*)sv.v, sv.probs, (float*)sv.o,
+                                 c.batch, c.seq, Hq, Hkv, D, s));
+    }
+    R_(proj_forward(e, l, P_O, sv.o, sv.h_mid, 0, sv.h_in, s));  // h_mid = h_in + attn
+    R_(rmsnorm_forward(sv.h_mid, w.norm2.data, e->bf ? nullptr : (float*)sv.xn2, e->bf ? (uint16_t*)sv.xn2 : nullptr,
+                       sv.rinv2, T, d, c.norm_eps, s));
+    R_(proj_forward(e, l, P_GU, sv.xn2, sv.gu, e->bf, nullptr, s));
+    R_(swiglu_fused_forward(sv.gu, sv.act, T, F, e->bf, s));
+    R_(proj_forward(e, l, P_D, sv.act, h_out, 0, sv.h_mid, s));  // h_out = h_mid + ffn
+  }
+  R_(rmsnorm_forward(e->h_fin, e->norm_f.data, e->bf ? nullptr : (float*)e->xnf, e->bf ? (uint16_t*)e->xnf : nullptr,
+                     e->rinv_f, T, d, c.norm_eps, s));
+  {  // tied LM head (BackpropEngine.cs:889-907)
+    GemmArgs g{};
+    g.precision = prec(e); g.alpha = 1.f; g.split_k = 1;
+    g.M = T; g.N = V; g.K = d;
+    g.A = act_k(e, e->xnf, d);
+    if (e->lora) g.B = Operand{e->emb_q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8_K : SRC_Q4K_K, e->emb_q.qs, e->emb_q.sc, d};
+    else g.B = e->emb.bf ? Operand{SRC_BF16_K, e->emb.bf, nullptr, d} : Operand{SRC_F32_K, e->emb.data, nullptr, d};
+    g.C = e->logits; g.ldc = V;
+    R_(gemm(g, s));
+  }
+  // loss + dLogits (CrossEntropyLoss.Compute / Backward, TrainLoop.cs:233-237)
+  if (e->bf) R_(ce_softmax_grad_bf16(e->logits, labels, (uint16_t*)e->dlogits, e->loss, T, V, -100, 0.f, s));
+  else R_(ce_softmax_grad(e->logits, labels, (float*)e->dlogits, e->loss, T, V, -100, 0.f, s));
+
+  // ---------------- backward
+  {  // head: dxnf = dLogits E ; dE += dLogits^T xnf (full)
+    GemmArgs g{};
+    g.precision = prec(e); g.alpha = 1.f; g.split_k = 1;
+    g.M = T; g.N = d; g.K = V;
+    g.A = act_k(e, e->dlogits, V);
+    if (e->lora) g.B = Operand{e->emb_q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8_R : SRC_Q4K_R, e->emb_q.qs, e->emb_q.sc, d};
+    else g.B = e->emb.bf ? Operand{SRC_BF16_R, e->emb.bf, nullptr, d} : Operand{SRC_F32_R, e->emb.data, nullptr, d};
+    g.C = e->dx; g.ldc = d;
+    g.split_k = split_for(T, d, V);
+    R_(gemm(g, s));
+    if (!e->lora) {
+      GemmArgs gw{};
+      gw.precision = prec(e); gw.alpha = 1.f; gw.beta = 1.f;
+      gw.M = V; gw.N = d; gw.K = T;
+      gw.A = act_r(e, e->dlogits, V);
+      gw.B = act_r(e, e->xnf, d);
+      gw.C = e->emb.grad; gw.ldc = d;
+      gw.split_k = split_for(V, d, T);
+      R_(gemm(gw, s));
+    }
+  }
+  // final norm (BackpropEngine.cs:168)
+  R_(rmsnorm_backward(e->dx, e->h_fin, 1, e->rinv_f, e->norm_f.data, e->norm_f.grad, e->dh, T, d, 0,
+                      e->bf ? (uint16_t*)e->dh_ta : nullptr, s));
+  for (int l = c.n_layers - 1; l >= 0; l--) {
+    Saved& sv = e->sv[l];
+    LayerW& w = e->L[l];
+    // FfnBackward (BackpropEngine.cs:623-657)
+    R_(proj_backward(e, l, P_D, e->dh_ta, e->dh, sv.act, e->dact, 0, nullptr, s));
+    R_(swiglu_fused_backward(e->dact, sv.gu, e->dgu, T, F, e->bf, s));
+    R_(proj_backward(e, l, P_GU, e->dgu, e->bf ? nullptr : (float*)e->dgu, sv.xn2, e->dx, 0, nullptr, s));
+    // norm2 backward, residual add into dh (BackpropEngine.cs:521-526)
+    R_(rmsnorm_backward(e->dx, sv.h_mid, 1, sv.rinv2, w.norm2.data, w.norm2.grad, e->dh, T, d, 1,
+                        e->bf ? (uint16_t*)e->dh_ta : nullptr, s));
+    // AttentionBackward (BackpropEngine.cs:539-602)
+    R_(proj_backward(e, l, P_O, e->dh_ta, e->dh, sv.o, nullptr, e->bf, e->dO, s));
+    if (e->bf) {
+      R_(flash_backward((const uint16_t*)sv.q, (const uint16_t*)sv.k, (const uint16_t*)sv.v, (const uint16_t*)sv.o,
+                        (const uint16_t*)e->dO, sv.lse, e->dq, e->dk, e->dv, c.batch, c.seq, Hq, Hkv, D, e->qd,
+                        e->kvd, e->kvd, e->qd, e->qd, e->qd, e->kvd, e->kvd, e->flash_ws, s));
+    } else {
+      R_(attention_probs_backward((const float*)e->dO, (const float*)sv.q, (const float*)sv.k, (const float*)sv.v,
+                                  sv.probs, e->dq, e->dk, e->dv, c.batch, c.seq, Hq, Hkv, D, s));
+    }
+    R_(qkv_prep_backward(e->dq, e->dk, e->dv, sv.qkv, sv.rinv_qk, c.qk_norm ? w.qn.data : nullptr,
+                         c.qk_norm ? w.kn.data : nullptr, c.qk_norm ? w.qn.grad : nullptr,
+                         c.qk_norm ? w.kn.grad : nullptr, e->cosT, e->sinT, e->dqkv, T, c.seq, Hq, Hkv, D,
+                         c.qk_norm, c.rope_neox, e->bf, s));
+    R_(proj_backward(e, l, P_QKV, e->dqkv, e->bf ? nullptr : (float*)e->dqkv, sv.xn1, e->dx, 0, nullptr, s));
+    R_(rmsnorm_backward(e->dx, sv.h_in, 1, sv.rinv1, w.norm1.data, w.norm1.grad, e->dh, T, d, 1,
+                        e->bf ? (uint16_t*)e->dh_ta : nullptr, s));
+  }
+  if (!e->lora) R_(embedding_backward(e->dh, ids, e->emb.grad, T, d, V, s));  // BackpropEngine.cs:203-205
+#undef R_
+  return SMHIP_OK;
+}
+
+static int optimizer_step(Engine* e, hipStream_t s) {
+  const smhip_model_config& c = e->c;
+  int rc;
+  e->step++;
+  if (c.max_grad_norm > 0.f) {  // TrainLoop.cs:125-127 -> Gradients.ClipGlobalNorm
+    if ((rc = l2normsq(e->grad, e->n_train, e->gnorm, 0, s))) return rc;
+    if ((rc = clip_grads(e->grad, e->n_train, e->gnorm, c.max_grad_norm, s))) return rc;
+  }
+  // AdamW.Update (AdamW.cs:52-89): bc_i = 1 - beta_i^t ; decayed tensors first, then no-decay
+  const float bc1 = 1.f - powf(c.beta1, (float)e->step), bc2 = 1.f - powf(c.beta2, (float)e->step);
+  if ((rc = adamw_update(e->train, e->grad, e->m, e->v, e->n_decay, c.beta1, c.beta2, bc1, bc2, c.lr, c.adam_eps,
+                         c.weight_decay, s)))
+    return rc;
+  if (e->n_train > e->n_decay)
+    if ((rc = adamw_update(e->train + e->n_decay, e->grad + e->n_decay, e->m + e->n_decay, e->v + e->n_decay,
+                           e->n_train - e->n_decay, c.beta1, c.beta2, bc1, bc2, c.lr, c.adam_eps, 0.f, s)))
+      return rc;
+  if (e->train_bf) return cast_bf16(e->train, e->train_bf, e->n_train, s);
+  return SMHIP_OK;
+}
+
+}  // namespace smhip
+
+using namespace smhip;
+
+extern "C" {
+
+int smhip_engine_create(const smhip_model_config* cfg, void** out) {
+  SMHIP_REQUIRE(cfg && out, "engine_create: null argument");
+  const smhip_model_config& c = *cfg;
+  SMHIP_REQUIRE(c.n_layers > 0 && c.d_model > 0 && c.n_heads > 0 && c.n_kv_heads > 0 && c.head_dim > 0 &&
+                    c.ffn_dim > 0 && c.vocab > 0 && c.batch > 0 && c.seq > 0,
+                "engine_create: non-positive dimension");
+  SMHIP_REQUIRE(c.n_heads % c.n_kv_heads == 0, "engine_create: n_heads must be a multiple of n_kv_heads");
+  SMHIP_REQUIRE(c.head_dim % 2 == 0 && c.head_dim <= 128, "engine_create: head_dim must be even and <= 128");
+  SMHIP_REQUIRE(c.precision == SMHIP_PREC_FP32 || c.precision == SMHIP_PREC_BF16, "engine_create: bad precision");
+  if (c.precision == SMHIP_PREC_BF16) {
+    SMHIP_REQUIRE(c.seq % 128 == 0 && (c.head_dim == 64 || c.head_dim == 128),
+                  "engine_create: bf16 mode needs seq % 128 == 0 and head_dim 64 or 128 (flash attention)");
+    SMHIP_REQUIRE(!c.use_bias, "engine_create: biases are supported in fp32 mode only");
+  }
+  if (c.lora_rank > 0) {
+    SMHIP_REQUIRE(c.base_qtype == SMHIP_QTYPE_Q8_0 || c.base_qtype == SMHIP_QTYPE_Q4_K,
+                  "engine_create: LoRA needs a Q8_0 or Q4_K base");
+    SMHIP_REQUIRE(!c.use_bias, "engine_create: LoRA bases are bias-free");
+    SMHIP_REQUIRE(c.d_model % 256 == 0 && c.ffn_dim % 256 == 0 && (c.n_heads * c.head_dim) % 256 == 0,
+                  "engine_create: quantised base needs dimensions that are multiples of 256");
+  } else {
+    SMHIP_REQUIRE(c.base_qtype == SMHIP_QTYPE_F32, "engine_create: full-parameter training needs an F32 base");
+  }
+  Engine* e = new Engine();
+  e->c = c;
+  int rc = build(e);
+  if (rc) {
+    for (void* p : e->allocs) hipFree(p);
+    delete e;
+    return rc;
+  }
+  *out = e;
+  return SMHIP_OK;
+}
+
+int smhip_engine_destroy(void* engine) {
+  if (!engine) return SMHIP_OK;
+  Engine* e = (Engine*)engine;
+  hipDeviceSynchronize();
+  for (void* p : e->allocs) hipFree(p);
+  delete e;
+  return SMHIP_OK;
+}
+
+int smhip_engine_param_count(void* engine, int64_t* trainable, int64_t* frozen) {
+  SMHIP_REQUIRE(engine, "engine: null handle");
+  Engine* e = (Engine*)engine;
+  int64_t tr = e->n_train, fr = e->n_frozen;
+  if (e->lora) {  // only diagonal blocks of fused B train
+    tr = 0;
+    for (int l = 0; l < e->c.n_layers; l++)
+      for (int p = 0; p < 4; p++) tr += (int64_t)e->In[p] * e->nr[p] + (int64_t)e->c.lora_rank * e->Out[p];
+    fr += (int64_t)e->c.vocab * e->c.d_model;
+    for (int p = 0; p < 4; p++) fr += (int64_t)e->c.n_layers * e->In[p] * e->Out[p];
+  }
+  if (trainable) *trainable = tr;
+  if (frozen) *frozen = fr;
+  return SMHIP_OK;
+}
+
+static int parse_layer(const char* name, int* layer, std::string* rest) {
+  if (name[0] != 'l' || !isdigit((unsigned char)name[1])) return 0;
+  const char* dot = strchr(name, '.');
+  if (!dot) return 0;
+  *layer = atoi(name + 1);
+  *rest = dot + 1;
+  return 1;
+}
+
+// LoRA tensor -> (fused projection, block index)
+static int lora_target(const std::string& rest, int* p, int* blk, int* isB) {
+  static const char* t[7] = {"q", "k", "v", "o", "gate", "up", "down"};
+  static const int proj[7] = {P_QKV, P_QKV, P_QKV, P_O, P_GU, P_GU, P_D};
+  static const int bl[7] = {0, 1, 2, 0, 0, 1, 0};
+  if (rest.rfind("lora.", 0) != 0) return 0;
+  for (int i = 0; i < 7; i++) {
+    std::string a = std::string("lora.") + t[i] + ".A", b = std::string("lora.") + t[i] + ".B";
+    if (rest == a || rest == b) { *p = proj[i]; *blk = bl[i]; *isB = rest == b; return 1; }
+  }
+  return 0;
+}
+
+// geometry of block blk of fused projection p: (In, Out, column offset in the fused output)
+static void block_geom(const Engine* e, int p, int blk, int* In, int* Out, int* coff) {
+  *In = e->In[p];
+  if (p == P_QKV) { const int o[3] = {0, e->qd, e->qd + e->kvd}, n[3] = {e->qd, e->kvd, e->kvd}; *Out = n[blk]; *coff = o[blk]; }
+  else if (p == P_GU) { *Out = e->c.ffn_dim; *coff = blk * e->c.ffn_dim; }
+  else { *Out = e->Out[p]; *coff = 0; }
+}
+
+int smhip_engine_set_tensor(void* engine, const char* name, const void* host, int64_t nbytes) {
+  SMHIP_REQUIRE(engine && name && host, "engine_set_tensor: null argument");
+  Engine* e = (Engine*)engine;
+  const int r = e->c.lora_rank;
+  int layer;
+  std::string rest;
+  // quantised base (LoRA mode): reference byte layout, repacked once
+  if (e->lora) {
+    static const char* wn[4] = {"wqkv", "wo", "wgu", "wd"};
+    QuantPlanes* q = nullptr;
+    if (!strcmp(name, "emb")) q = &e->emb_q;
+    else if (parse_layer(name, &layer, &rest) && layer < e->c.n_layers)
+      for (int p = 0; p < 4; p++) if (rest == wn[p]) q = &e->L[layer].q[p];
+    if (q) {
+      const int64_t bpb = q->kind == SMHIP_QTYPE_Q8_0 ? 34 : 144, epb = q->kind == SMHIP_QTYPE_Q8_0 ? 32 : 256;
+      SMHIP_REQUIRE(nbytes == q->n / epb * bpb, "engine_set_tensor: quantised byte count does not match the shape");
+      void* tmp = nullptr;
+      SMHIP_CHECK_HIP(hipMalloc(&tmp, nbytes));
+      hipMemcpy(tmp, host, nbytes, hipMemcpyHostToDevice);
+      QuantPlanes out;
+      int rc = repack_planes(q->kind, tmp, q->n, q->qs, &out, nullptr);
+      hipDeviceSynchronize();
+      hipFree(tmp);
+      return rc;
+    }
+    int p, blk, isB;
+    if (parse_layer(name, &layer, &rest) && layer < e->c.n_layers && lora_target(rest, &p, &blk, &isB)) {
+      int In, Out, coff;
+      block_geom(e, p, blk, &In, &Out, &coff);
+      LayerW& w = e->L[layer];
+      if (!isB) {  // A_blk [In, r] -> columns blk*r.. of A [In, nr]
+        SMHIP_REQUIRE(nbytes == (int64_t)In * r * 4, "engine_set_tensor: LoRA A size mismatch");
+        SMHIP_CHECK_HIP(hipMemcpy2D(w.la[p].data + blk * r, sizeof(float) * e->nr[p], host, sizeof(float) * r,
+                                    sizeof(float) * r, In, hipMemcpyHostToDevice));
+      } else {  // B_blk [r, Out] -> rows blk*r.., columns coff.. of B [nr, OutF]
+        SMHIP_REQUIRE(nbytes == (int64_t)r * Out * 4, "engine_set_tensor: LoRA B size mismatch");
+        SMHIP_CHECK_HIP(hipMemcpy2D(w.lb[p].data + (int64_t)blk * r * e->Out[p] + coff, sizeof(float) * e->Out[p], host,
+                                    sizeof(float) * Out, sizeof(float) * Out, r, hipMemcpyHostToDevice));
+      }
+      return SMHIP_OK;
+    }
+  }
+  auto it = e->dense_by_name.find(name);
+  SMHIP_REQUIRE(it != e->dense_by_name.end(), std::string("engine_set_tensor: unknown tensor ") + name);
+  DenseRef* d = it->second;
+  SMHIP_REQUIRE(nbytes == d->n * 4, std::string("engine_set_tensor: size mismatch for ") + name);
+  SMHIP_CHECK_HIP(hipMemcpy(d->data, host, nbytes, hipMemcpyHostToDevice));
+  if (d->bf) return cast_bf16(d->data, d->bf, d->n, nullptr);
+  return SMHIP_OK;
+}
+
+int smhip_engine_get_tensor(void* engine, const char* name, int which, void* host, int64_t nbytes) {
+  SMHIP_REQUIRE(engine && name && host, "engine_get_tensor: null argument");
+  Engine* e = (Engine*)engine;
+  SMHIP_CHECK_HIP(hipDeviceSynchronize());
+  const int r = e->c.lora_rank;
+  int layer, p, blk, isB;
+  std::string rest;
+  if (e->lora && parse_layer(name, &layer, &rest) && layer < e->c.n_layers && lora_target(rest, &p, &blk, &isB)) {
+    int In, Out, coff;
+    block_geom(e, p, blk, &In, &Out, &coff);
+    LayerW& w = e->L[layer];
+    const float* base = which ? (isB ? w.lb[p].grad : w.la[p].grad) : (isB ? w.lb[p].data : w.la[p].data);
+    if (!isB) {
+      SMHIP_REQUIRE(nbytes == (int64_t)In * r * 4, "engine_get_tensor: LoRA A size mismatch");
+      SMHIP_CHECK_HIP(hipMemcpy2D(host, sizeof(float) * r, base + blk * r, sizeof(float) * e->nr[p], sizeof(float) * r,
+                                  In, hipMemcpyDeviceToHost));
+    } else {
+      SMHIP_REQUIRE(nbytes == (int64_t)r * Out * 4, "engine_get_tensor: LoRA B size mismatch");
+      SMHIP_CHECK_HIP(hipMemcpy2D(host, sizeof(float) * Out, base + (int64_t)blk * r * e->Out[p] + coff,
+                                  sizeof(float) * e->Out[p], sizeof(float) * Out, r, hipMemcpyDeviceToHost));
+    }
+    return SMHIP_OK;
+  }
+  auto it = e->dense_by_name.find(name);
+  SMHIP_REQUIRE(it != e->dense_by_name.end(), std::string("engine_get_tensor: unknown tensor ") + name);
+  DenseRef* d = it->second;
+  SMHIP_REQUIRE(nbytes == d->n * 4, std::string("engine_get_tensor: size mismatch for ") + name);
+  const float* src = which ? d->grad : d->data;
+  SMHIP_REQUIRE(src, std::string("engine_get_tensor: no gradient for frozen tensor ") + name);
+  SMHIP_CHECK_HIP(hipMemcpy(host, src, nbytes, hipMemcpyDeviceToHost));
+  return SMHIP_OK;
+}
+
+int smhip_engine_init_synthetic(void* engine, uint64_t seed) {
+  SMHIP_REQUIRE(engine, "engine: null handle");
+  Engine* e = (Engine*)engine;
+  const smhip_model_config& c = e->c;
+  hipStream_t s = nullptr;
+  int rc;
+  uint64_t sd = seed * 1000003ull;
+  auto next = [&]() { return ++sd; };
+  // norms = 1 (ModelFactory.cs:178-181), biases = 0
+  auto ones = [&](DenseRef& d) { return d.n ? fill_normal(d.data, d.n, next(), 1.f, 0.f, s) : 0; };
+  if ((rc = ones(e->norm_f))) return rc;
+  for (auto& w : e->L) {
+    if ((rc = ones(w.norm1)) || (rc = ones(w.norm2))) return rc;
+    if (c.qk_norm && ((rc = ones(w.qn)) || (rc = ones(w.kn)))) return rc;
+  }
+  if (!e->lora) {  // WeightInitializer.InitializeRandomly: N(0, 0.02) (WeightInitializer.cs:23-45)
+    if ((rc = fill_normal(e->emb.data, e->emb.n, next(), 0.f, 0.02f, s))) return rc;
+    for (auto& w : e->L)
+      for (int p = 0; p < 4; p++) {
+        if ((rc = fill_normal(w.w[p].data, w.w[p].n, next(), 0.f, 0.02f, s))) return rc;
+        if (c.use_bias && (rc = zero_bytes(w.b[p].data, sizeof(float) * w.b[p].n, s))) return rc;
+      }
+    if (e->train_bf) rc = cast_bf16(e->train, e->train_bf, e->n_train, s);
+    return rc ? rc : (hipDeviceSynchronize() == hipSuccess ? SMHIP_OK : fail(SMHIP_EHIP, "init_synthetic"));
+  }
+  // LoRA: base N(0, 0.02) quantised with the TensorQuantizer encoders, repacked to planes
+  int64_t maxn = (int64_t)c.vocab * c.d_model;
+  for (int p = 0; p < 4; p++) maxn = std::max<int64_t>(maxn, (int64_t)e->In[p] * e->Out[p]);
+  float* tmpf = nullptr;
+  void* tmpq = nullptr;
+  SMHIP_CHECK_HIP(hipMalloc(&tmpf, sizeof(float) * maxn));
+  SMHIP_CHECK_HIP(hipMalloc(&tmpq, (size_t)maxn / 32 * 34 + 256));
+  auto quant = [&](QuantPlanes& q) -> int {
+    int r2;
+    if ((r2 = fill_normal(tmpf, q.n, next(), 0.f, 0.02f, s))) return r2;
+    if ((r2 = encode_quant(q.kind, tmpf, q.n, tmpq, s))) return r2;
+    QuantPlanes o;
+    return repack_planes(q.kind, tmpq, q.n, q.qs, &o, s);
+  };
+  rc = quant(e->emb_q);
+  for (int l = 0; l < c.n_layers && !rc; l++)
+    for (int p = 0; p < 4 && !rc; p++) rc = quant(e->L[l].q[p]);
+  hipDeviceSynchronize();
+  hipFree(tmpf);
+  hipFree(tmpq);
+  if (rc) return rc;
+  // adapters: A ~ Kaiming-uniform U(-1/sqrt(In), 1/sqrt(In)), B = 0 then + N(0, 1e-3), off-diagonal blocks 0
+  for (auto& w : e->L)
+    for (int p = 0; p < 4; p++) {
+      const float bound = 1.f / sqrtf((float)e->In[p]);
+      if ((rc = fill_uniform(w.la[p].data, w.la[p].n, next(), -bound, bound, s))) return rc;
+      if ((rc = fill_normal(w.lb[p].data, w.lb[p].n, next(), 0.f, 1e-3f, s))) return rc;
+      if (e->nblk[p] > 1)
+        if ((rc = lora_mask(w.lb[p].data, e->nr[p], c.lora_rank, e->Out[p], p == P_QKV ? w.lb_cols : w.lb_cols + 3,
+                            p == P_QKV ? 3 : 2, s)))
+          return rc;
+    }
+  return hipDeviceSynchronize() == hipSuccess ? SMHIP_OK : fail(SMHIP_EHIP, "init_synthetic");
+}
+
+int smhip_engine_forward_backward(void* engine, const int32_t* ids, const int32_t* labels, float* loss,
+                                  smhip_stream_t stream) {
+  SMHIP_REQUIRE(engine && ids && labels, "engine_forward_backward: null argument");
+  Engine* e = (Engine*)engine;
+  int rc = forward_backward(e, ids, labels, (hipStream_t)stream);
+  if (rc) return rc;
+  if (loss) SMHIP_CHECK_HIP(hipMemcpyAsync(loss, e->loss, sizeof(float), hipMemcpyDeviceToDevice, (hipStream_t)stream));
+  return SMHIP_OK;
+}
+
+int smhip_engine_optimizer_step(void* engine, float* grad_norm_sq, smhip_stream_t stream) {
+  SMHIP_REQUIRE(engine, "engine: null handle");
+  Engine* e = (Engine*)engine;
+  int rc = optimizer_step(e, (hipStream_t)stream);
+  if (rc) return rc;
+  if (grad_norm_sq)
+    SMHIP_CHECK_HIP(hipMemcpyAsync(grad_norm_sq, e->gnorm, sizeof(float), hipMemcpyDeviceToDevice, (hipStream_t)stream));
+  return SMHIP_OK;
+}
+
+int smhip_engine_step(void* engine, const int32_t* ids, const int32_t* labels, float* loss, smhip_stream_t stream) {
+  int rc = smhip_engine_forward_backward(engine, ids, labels, loss, stream);
+  if (rc) return rc;
+  return smhip_engine_optimizer_step(engine, nullptr, stream);
+}
+
+int smhip_engine_read_activation(void* engine, const char* what, int layer, void* host, int64_t nbytes) {
+  SMHIP_REQUIRE(engine && what && host, "engine_read_activation: null argument");
+  Engine* e = (Engine*)engine;
+  SMHIP_REQUIRE(layer >= 0 && layer < e->c.n_layers, "engine_read_activation: bad layer");
+  const Saved& s = e->sv[layer];
+  const int64_t T = e->T, d = e->c.d_model, F = e->c.ffn_dim;
+  const void* src = nullptr;
+  int64_t bytes = 0;
+  const int64_t es = (int64_t)e->esz;
+  std::string w(what);
+  if (w == "h_in") { src = s.h_in; bytes = T * d * 4; }
+  else if (w == "h_mid") { src = s.h_mid; bytes = T * d * 4; }
+  else if (w == "xn1") { src = s.xn1; bytes = T * d * es; }
+  else if (w == "qkv") { src = s.qkv; bytes = T * e->nqkv * 4; }
+  else if (w == "q") { src = s.q; bytes = T * e->qd * es; }
+  else if (w == "k") { src = s.k; bytes = T * e->kvd * es; }
+  else if (w == "v") { src = s.v; bytes = T * e->kvd * es; }
+  else if (w == "o") { src = s.o; bytes = T * e->qd * es; }
+  else if (w == "gu") { src = s.gu; bytes = T * 2 * F * es; }
+  else if (w == "act") { src = s.act; bytes = T * F * es; }
+  else if (w == "h_fin") { src = e->h_fin; bytes = T * d * 4; }
+  else if (w == "logits") { src = e->logits; bytes = T * e->c.vocab * 4; }
+  else return fail(SMHIP_EINVAL, "engine_read_activation: unknown activation " + w);
+  SMHIP_REQUIRE(nbytes == bytes, "engine_read_activation: size mismatch for " + w);
+  SMHIP_CHECK_HIP(hipDeviceSynchronize());
+  SMHIP_CHECK_HIP(hipMemcpy(host, src, bytes, hipMemcpyDeviceToHost));
+  return SMHIP_OK;
+}
+
+int smhip_fill_token_ids(int32_t* ids, int64_t n, uint64_t seed, int vocab, smhip_stream_t stream) {
+  SMHIP_REQUIRE(ids && n >= 0 && vocab > 0, "fill_token_ids: bad arguments");
+  return fill_ids(ids, n, seed, vocab, (hipStream_t)stream);
+}
+
+int smhip_quantize(int qtype, const float* x, int64_t n, void* out, smhip_stream_t stream) {
+  SMHIP_REQUIRE(x && out && n >= 0, "quantize: bad arguments");
+  return encode_quant(qtype, x, n, out, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,439 @@
+// engine_kernels.hip — fused elementwise kernels used by the training engine.
+//
+//  * qk_norm + RoPE forward / backward on the fused q|k|v projection output
+//    (per-head RMSNorm as in AttentionLayer.cs:284, then RoPE.cs:168-259; the
+//    backward is RoPE.cs:300-347 followed by the RMSNorm-slot formula
+//    GradientKernels.cs:303-337 applied per head row);
+//  * SwiGLU forward/backward on the fused [gate | up] row layout
+//    (BackpropEngine.cs:409-431 forward, :623-657 backward);
+//  * LoRA block-diagonal gradient masking, global-norm clipping
+//    (Gradients.cs:92-116), bf16 shadow casts;
+//  * synthetic initialisation: a counter-based normal generator and the
+//    Q8_0 / Q4_K encoders of TensorQuantizer (TensorQuantizer.cs:80-144,
+//    TensorQuantizer.KQuant.cs:173-225,451-459) so quantised bases are built
+//    on the device with the reference's exact bytes.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace smhip {
+
+template <typename T> __device__ inline void st(T* p, float v);
+template <> __device__ inline void st<float>(float* p, float v) { *p = v; }
+template <> __device__ inline void st<uint16_t>(uint16_t* p, float v) { *p = f2bf(v); }
+template <typename T> __device__ inline float ldv(const T* p);
+template <> __device__ inline float ldv<float>(const float* p) { return *p; }
+template <> __device__ inline float ldv<uint16_t>(const uint16_t* p) { return bf2f(*p); }
+
+static int gridn(int64_t n, int per = 256, int cap = 8) {
+  int64_t g = (n + per - 1) / per;
+  int64_t c = (int64_t)num_cus() * cap;
+  return (int)std::max<int64_t>(1, std::min(g, c));
+}
+
+// ============================================================================
+// q/k/v split + optional per-head RMSNorm + RoPE.  One wave per (token, head) row;
+// rows 0..Hq-1 are query heads, Hq..Hq+Hkv-1 key heads, then Hkv value heads.
+// ============================================================================
+template <typename TA>
+__global__ __launch_bounds__(256) void qkv_prep_fwd_kernel(
+    const float* __restrict__ qkv, TA* __restrict__ qo, TA* __restrict__ ko, TA* __restrict__ vo,
+    float* __restrict__ rinv, const float* __restrict__ wq, const float* __restrict__ wk,
+    const float* __restrict__ cosT, const float* __restrict__ sinT, int T, int S, int Hq, int Hkv,
+    int D, int qk_norm, int neox, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int H = Hq + 2 * Hkv, nqkv = H * D;
+  const int64_t rows = (int64_t)T * H;
+  const int pairs = D / 2;
+  for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += (int64_t)gridDim.x * 4) {
+    const int t = (int)(r / H), hh = (int)(r % H);
+    const float* x = qkv + (int64_t)t * nqkv + hh * D;
+    if (hh >= Hq + Hkv) {  // value head: copy
+      TA* dst = vo + (int64_t)t * Hkv * D + (hh - Hq - Hkv) * D;
+      for (int d = lane; d < D; d += 64) st(dst + d, x[d]);
+      continue;
+    }
+    const bool isq = hh < Hq;
+    const float* w = isq ? wq : wk;
+    TA* dst = isq ? qo + (int64_t)t * Hq * D + hh * D : ko + (int64_t)t * Hkv * D + (hh - Hq) * D;
+    float ri = 1.f;
+    if (qk_norm) {
+      float ss = 0.f;
+      for (int d = lane; d < D; d += 64) ss += x[d] * x[d];
+      ss = wave_sum(ss);
+      ri = 1.f / sqrtf(ss / (float)D + eps);
+      if (lane == 0) rinv[(int64_t)t * (Hq + Hkv) + hh] = ri;
+    }
+    const int pos = t % S;
+    for (int p = lane; p < pairs; p += 64) {
+      const int i0 = neox ? p : 2 * p, i1 = neox ? p + pairs : 2 * p + 1;
+      float a = x[i0], b = x[i1];
+      if (qk_norm) {
+        a = a * ri * w[i0];
+        b = b * ri * w[i1];
+      }
+      const float c = cosT[(int64_t)pos * pairs + p], sn = sinT[(int64_t)pos * pairs + p];
+      st(dst + i0, a * c - b * sn);
+      st(dst + i1, b * c + a * sn);
+    }
+  }
+}
+
+// Backward: dq/dk/dv (fp32, attention outputs) -> dqkv (TA) fused [T, nqkv];
+// dwq/dwk partials per block (deterministic, reduced afterwards).
+template <typename TA>
+__global__ __launch_bounds__(256) void qkv_prep_bwd_kernel(
+    const float* __restrict__ dq, const float* __restrict__ dk, const float* __restrict__ dv,
+    const float* __restrict__ qkv, const float* __restrict__ rinv, const float* __restrict__ wq,
+    const float* __restrict__ wk, const float* __restrict__ cosT, const float* __restrict__ sinT,
+    TA* __restrict__ dqkv, float* __restrict__ part, int T, int S, int Hq, int Hkv, int D, int qk_norm,
+    int neox) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int H = Hq + 2 * Hkv, nqkv = H * D;
+  const int64_t rows = (int64_t)T * H;
+  const int pairs = D / 2;
+  // per-lane dw accumulators for columns lane, lane+64 (D <= 128) of q and k weights
+  float aq0 = 0.f, aq1 = 0.f, ak0 = 0.f, ak1 = 0.f;
+  for (int64_t r = (int64_t)blockIdx.x * 4 + wv; r < rows; r += (int64_t)gridDim.x * 4) {
+    const int t = (int)(r / H), hh = (int)(r % H);
+    TA* dst = dqkv + (int64_t)t * nqkv + hh * D;
+    if (hh >= Hq + Hkv) {
+      const float* g = dv + (int64_t)t * Hkv * D + (hh - Hq - Hkv) * D;
+      for (int d = lane; d < D; d += 64) st(dst + d, g[d]);
+      continue;
+    }
+    const bool isq = hh < Hq;
+    const float* g = isq ? dq + (int64_t)t * Hq * D + hh * D : dk + (int64_t)t * Hkv * D + (hh - Hq) * D;
+    const int pos = t % S;
+    // inverse rotation into registers: element d = lane + 64*j
+    float gr[2] = {0.f, 0.f};
+    for (int j = 0; j < 2; j++) {
+      const int d = lane + 64 * j;
+      if (d >= D) break;
+      int p, first;
+      if (neox) { p = d < pairs ? d : d - pairs; first = d < pairs; }
+      else { p = d >> 1; first = (d & 1) == 0; }
+      const int i0 = neox ? p : 2 * p, i1 = neox ? p + pairs : 2 * p + 1;
+      const float c = cosT[(int64_t)pos * pairs + p], sn = sinT[(int64_t)pos * pairs + p];
+      const float g0 = g[i0], g1 = g[i1];
+      gr[j] = first ? c * g0 + sn * g1 : -sn * g0 + c * g1;
+    }
+    if (!qk_norm) {
+      for (int j = 0; j < 2; j++) if (lane + 64 * j < D) st(dst + lane + 64 * j, gr[j]);
+      continue;
+    }
+    const float* x = qkv + (int64_t)t * nqkv + hh * D;
+    const float* w = isq ? wq : wk;
+    const float ri = rinv[(int64_t)t * (Hq + Hkv) + hh];
+    float xn[2] = {0.f, 0.f}, dot = 0.f;
+    for (int j = 0; j < 2; j++) {
+      const int d = lane + 64 * j;
+      if (d >= D) break;
+      xn[j] = x[d] * ri;
+      dot += gr[j] * w[d] * xn[j];
+      if (isq) { if (j == 0) aq0 += gr[j] * xn[j]; else aq1 += gr[j] * xn[j]; }
+      else { if (j == 0) ak0 += gr[j] * xn[j]; else ak1 += gr[j] * xn[j]; }
+    }
+    dot = wave_sum(dot) / (float)D;
+    for (int j = 0; j < 2; j++) {
+      const int d = lane + 64 * j;
+      if (d >= D) break;
+      st(dst + d, ri * (gr[j] * w[d] - xn[j] * dot));
+    }
+  }
+  if (part) {
+    __shared__ float sh[4][4][64];
+    sh[wv][0][lane] = aq0; sh[wv][1][lane] = aq1; sh[wv][2][lane] = ak0; sh[wv][3][lane] = ak1;
+    __syncthreads();
+    if (threadIdx.x < 4 * 64) {
+      const int which = threadIdx.x >> 6, l = threadIdx.x & 63;
+      float s = sh[0][which][l] + sh[1][which][l] + sh[2][which][l] + sh[3][which][l];
+      const int col = (which & 1) * 64 + l;  // column within head
+      if (col < D) part[(int64_t)blockIdx.x * 2 * D + (which >> 1) * D + col] = s;
+    }
+  }
+}
+
+__global__ void colsum_add2_kernel(const float* __restrict__ part, float* __restrict__ dq,
+                                   float* __restrict__ dk, int G, int D) {
+  int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= 2 * D) return;
+  float s = 0.f;
+  for (int g = 0; g < G; g++) s += part[(int64_t)g * 2 * D + c];
+  float* dst = c < D ? dq + c : dk + (c - D);
+  *dst += s;
+}
+
+int qkv_prep_forward(const float* qkv, void* q, void* k, void* v, float* rinv, const float* wq,
+                     const float* wk, const float* cosT, const float* sinT, int T, int S, int Hq, int Hkv,
+                     int D, int qk_norm, int neox, float eps, int bf16, hipStream_t s) {
+  SMHIP_REQUIRE(D <= 128 && D % 2 == 0, "qkv prep: head_dim must be even and <= 128");
+  const int64_t rows = (int64_t)T * (Hq + 2 * Hkv);
+  const int g = gridn(rows, 4);
+  if (bf16)
+    hipLaunchKernelGGL(qkv_prep_fwd_kernel<uint16_t>, dim3(g), dim3(256), 0, s, qkv, (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, rinv, wq, wk, cosT, sinT, T, S, Hq, Hkv, D, qk_norm, neox, eps);
+  else
+    hipLaunchKernelGGL(qkv_prep_fwd_kernel<float>, dim3(g), dim3(256), 0, s, qkv, (float*)q, (float*)k, (float*)v, rinv, wq, wk, cosT, sinT, T, S, Hq, Hkv, D, qk_norm, neox, eps);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+int qkv_prep_backward(const float* dq, const float* dk, const float* dv, const float* qkv, const float* rinv,
+                      const float* wq, const float* wk, float* dwq, float* dwk, const float* cosT,
+                      const float* sinT, void* dqkv, int T, int S, int Hq, int Hkv, int D, int qk_norm,
+                      int neox, int bf16, hipStream_t s) {
+  SMHIP_REQUIRE(D <= 128 && D % 2 == 0, "qkv prep: head_dim must be even and <= 128");
+  const int64_t rows = (int64_t)T * (Hq + 2 * Hkv);
+  const int g = gridn(rows, 4, 2);
+  float* part = nullptr;
+  if (qk_norm && (dwq || dwk)) {
+    part = (float*)workspace(s, sizeof(float) * (size_t)g * 2 * D, 7);
+    if (!part) return fail(SMHIP_ENOMEM, "qkv prep backward: workspace");
+  }
+  if (bf16)
+    hipLaunchKernelGGL(qkv_prep_bwd_kernel<uint16_t>, dim3(g), dim3(256), 0, s, dq, dk, dv, qkv, rinv, wq, wk, cosT, sinT, (uint16_t*)dqkv, part, T, S, Hq, Hkv, D, qk_norm, neox);
+  else
+    hipLaunchKernelGGL(qkv_prep_bwd_kernel<float>, dim3(g), dim3(256), 0, s, dq, dk, dv, qkv, rinv, wq, wk, cosT, sinT, (float*)dqkv, part, T, S, Hq, Hkv, D, qk_norm, neox);
+  SMHIP_CHECK_LAUNCH();
+  if (part) {
+    hipLaunchKernelGGL(colsum_add2_kernel, dim3(ceil_div(2 * D, 256)), dim3(256), 0, s, part, dwq, dwk, g, D);
+    SMHIP_CHECK_LAUNCH();
+  }
+  return SMHIP_OK;
+}
+
+// ============================================================================
+// SwiGLU on the fused [gate | up] layout
+// ============================================================================
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void swiglu_fused_fwd_kernel(const TI* __restrict__ gu, TO* __restrict__ act, int T, int F) {
+  const int64_t n = (int64_t)T * F;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t t = i / F, d = i - t * F;
+    const float g = ldv(gu + t * 2 * F + d), u = ldv(gu + t * 2 * F + F + d);
+    st(act + i, (g / (1.f + expf(-g))) * u);
+  }
+}
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void swiglu_fused_bwd_kernel(const float* __restrict__ dA, const TI* __restrict__ gu,
+                                                               TO* __restrict__ dgu, int T, int F) {
+  const int64_t n = (int64_t)T * F;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t t = i / F, d = i - t * F;
+    const float g = ldv(gu + t * 2 * F + d), u = ldv(gu + t * 2 * F + F + d), da = dA[i];
+    const float sig = 1.f / (1.f + expf(-g));
+    st(dgu + t * 2 * F + F + d, da * (g * sig));
+    st(dgu + t * 2 * F + d, da * (sig * (1.f + g * (1.f - sig))) * u);
+  }
+}
+
+int swiglu_fused_forward(const void* gu, void* act, int T, int F, int bf16, hipStream_t s) {
+  const int g = gridn((int64_t)T * F);
+  if (bf16) hipLaunchKernelGGL((swiglu_fused_fwd_kernel<uint16_t, uint16_t>), dim3(g), dim3(256), 0, s, (const uint16_t*)gu, (uint16_t*)act, T, F);
+  else hipLaunchKernelGGL((swiglu_fused_fwd_kernel<float, float>), dim3(g), dim3(256), 0, s, (const float*)gu, (float*)act, T, F);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+int swiglu_fused_backward(const float* dA, const void* gu, void* dgu, int T, int F, int bf16, hipStream_t s) {
+  const int g = gridn((int64_t)T * F);
+  if (bf16) hipLaunchKernelGGL((swiglu_fused_bwd_kernel<uint16_t, uint16_t>), dim3(g), dim3(256), 0, s, dA, (const uint16_t*)gu, (uint16_t*)dgu, T, F);
+  else hipLaunchKernelGGL((swiglu_fused_bwd_kernel<float, float>), dim3(g), dim3(256), 0, s, dA, (const float*)gu, (float*)dgu, T, F);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// ============================================================================
+// LoRA block-diagonal mask: zero dB[j, n] unless row block (j / r) == column block
+// ============================================================================
+__global__ void lora_mask_kernel(float* __restrict__ dB, int nr, int r, int Out, const int* __restrict__ col_starts,
+                                 int nblocks) {
+  const int64_t n = (int64_t)nr * Out;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int j = (int)(i / Out), c = (int)(i % Out);
+    const int blk = j / r;
+    const int lo = col_starts[blk], hi = blk + 1 < nblocks ? col_starts[blk + 1] : Out;
+    if (c < lo || c >= hi) dB[i] = 0.f;
+  }
+}
+int lora_mask(float* dB, int nr, int r, int Out, const int* col_starts_dev, int nblocks, hipStream_t s) {
+  hipLaunchKernelGGL(lora_mask_kernel, dim3(gridn((int64_t)nr * Out)), dim3(256), 0, s, dB, nr, r, Out, col_starts_dev, nblocks);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// ============================================================================
+// clipping (Gradients.ClipGlobalNorm, Gradients.cs:92-116): if ||g|| > max, g *= max/||g||
+// norm_sq is a device float holding sum g^2 (smhip l2normsq), also exported for logging.
+// ============================================================================
+__global__ void clip_kernel(float* __restrict__ g, int64_t n, const float* __restrict__ norm_sq, float max_norm) {
+  const float nrm = sqrtf(*norm_sq);
+  if (!(nrm > max_norm)) return;
+  const float sc = max_norm / nrm;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) g[i] *= sc;
+}
+int clip_grads(float* g, int64_t n, const float* norm_sq, float max_norm, hipStream_t s) {
+  hipLaunchKernelGGL(clip_kernel, dim3(gridn(n)), dim3(256), 0, s, g, n, norm_sq, max_norm);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+__global__ void cast_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) y[i] = f2bf(x[i]);
+}
+int cast_bf16(const float* x, uint16_t* y, int64_t n, hipStream_t s) {
+  if (n <= 0) return SMHIP_OK;
+  hipLaunchKernelGGL(cast_bf16_kernel, dim3(gridn(n)), dim3(256), 0, s, x, y, n);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// ============================================================================
+// synthetic data: counter-based normal generator (splitmix64 hash of (seed, index),
+// Box-Muller in double) and uniform integers for token ids
+// ============================================================================
+__device__ inline uint64_t mix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+__global__ void fill_normal_kernel(float* __restrict__ x, int64_t n, uint64_t seed, float mean, float std) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    uint64_t a = mix64(seed * 0x100000001B3ull + 2 * (uint64_t)i), b = mix64(seed * 0x100000001B3ull + 2 * (uint64_t)i + 1);
+    double u1 = ((a >> 11) + 1) * (1.0 / 9007199254740993.0);
+    double u2 = (b >> 11) * (1.0 / 9007199254740992.0);
+    x[i] = mean + std * (float)(sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2));
+  }
+}
+__global__ void fill_uniform_kernel(float* __restrict__ x, int64_t n, uint64_t seed, float lo, float hi) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    double u = (mix64(seed * 0x100000001B3ull + (uint64_t)i) >> 11) * (1.0 / 9007199254740992.0);
+    x[i] = lo + (hi - lo) * (float)u;
+  }
+}
+__global__ void fill_ids_kernel(int32_t* __restrict__ x, int64_t n, uint64_t seed, int V) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    x[i] = (int32_t)(mix64(seed * 0x100000001B3ull + (uint64_t)i) % (uint64_t)V);
+}
+int fill_normal(float* x, int64_t n, uint64_t seed, float mean, float std, hipStream_t s) {
+  hipLaunchKernelGGL(fill_normal_kernel, dim3(gridn(n)), dim3(256), 0, s, x, n, seed, mean, std);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+int fill_uniform(float* x, int64_t n, uint64_t seed, float lo, float hi, hipStream_t s) {
+  hipLaunchKernelGGL(fill_uniform_kernel, dim3(gridn(n)), dim3(256), 0, s, x, n, seed, lo, hi);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+int fill_ids(int32_t* x, int64_t n, uint64_t seed, int V, hipStream_t s) {
+  hipLaunchKernelGGL(fill_ids_kernel, dim3(gridn(n)), dim3(256), 0, s, x, n, seed, V);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+// ============================================================================
+// encoders (bit-identical to the reference byte layout)
+// ============================================================================
+// float -> IEEE binary16 bits, round to nearest even ((Half)f, QuantizationKernels.cs:149)
+__device__ inline uint16_t f2h_rne(float f) {
+  uint32_t x = __builtin_bit_cast(uint32_t, f);
+  uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7FFFFFFFu;
+  if (ax >= 0x7F800000u) return (uint16_t)(sign | (ax == 0x7F800000u ? 0x7C00u : (0x7E00u | ((ax >> 13) & 0x3FFu))));
+  if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);
+  if (ax >= 0x38800000u) {
+    uint32_t mant = ax & 0x7FFFFFu, h = (((ax >> 23) - 112) << 10) | (mant >> 13), rem = mant & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+  }
+  if (ax < 0x33000000u) return (uint16_t)sign;
+  uint32_t mant = (ax & 0x7FFFFFu) | 0x800000u;
+  int shift = 126 - (int)(ax >> 23);
+  uint32_t h = mant >> shift, rem = mant & ((1u << shift) - 1u), half = 1u << (shift - 1);
+  if (rem > half || (rem == half && (h & 1u))) h++;
+  return (uint16_t)(sign | h);
+}
+__device__ inline int round_away(float x) { return (int)roundf(x); }
+__device__ inline int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+__global__ void encode_q8_0_kernel(const float* __restrict__ x, uint8_t* __restrict__ out, int64_t nb) {
+  for (int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x; b < nb; b += (int64_t)gridDim.x * 256) {
+    const float* v = x + b * 32;
+    uint8_t* o = out + b * 34;
+    float amax = 0.f;
+    for (int j = 0; j < 32; j++) { float a = fabsf(v[j]); if (a > amax) amax = a; }
+    if (amax == 0.f) {
+      for (int j = 0; j < 34; j++) o[j] = 0;
+      continue;
+    }
+    const float d = amax / 127.f;
+    const uint16_t h = f2h_rne(d);
+    o[0] = (uint8_t)h;
+    o[1] = (uint8_t)(h >> 8);
+    for (int j = 0; j < 32; j++) o[2 + j] = (uint8_t)(int8_t)clampi(round_away(v[j] / d), -128, 127);
+  }
+}
+
+__global__ void encode_q4k_kernel(const float* __restrict__ x, uint8_t* __restrict__ out, int64_t nb) {
+  for (int64_t b = (int64_t)blockIdx.x * 64 + threadIdx.x; b < nb; b += (int64_t)gridDim.x * 64) {
+    const float* v = x + b * 256;
+    uint8_t* o = out + b * 144;
+    for (int j = 0; j < 144; j++) o[j] = 0;
+    float amax = 0.f;
+    for (int j = 0; j < 256; j++) { float a = fabsf(v[j]); if (a > amax) amax = a; }
+    if (amax == 0.f) continue;
+    const float step = amax / 63.f;
+    const uint16_t h = f2h_rne(step);
+    o[0] = o[2] = (uint8_t)h;
+    o[1] = o[3] = (uint8_t)(h >> 8);
+    int sc[8], mn[8];
+    for (int sub = 0; sub < 8; sub++) {
+      const float* g = v + sub * 32;
+      float gmn = 3.40282347e+38f, gmx = -3.40282347e+38f;
+      for (int j = 0; j < 32; j++) { if (g[j] < gmn) gmn = g[j]; if (g[j] > gmx) gmx = g[j]; }
+      const float range = gmx - gmn;
+      mn[sub] = clampi(round_away(-gmn / step), 0, 63);
+      if (range <= 0.f) { sc[sub] = 0; continue; }
+      sc[sub] = clampi(round_away(range / (15.f * step)), 1, 63);
+      const float scF = (float)sc[sub] * step;
+      for (int j = 0; j < 32; j++) {
+        const int code = clampi(round_away((g[j] + (float)mn[sub] * step) / scF), 0, 15);
+        const int i = sub * 32 + j;
+        o[16 + (i / 64) * 32 + (i % 32)] |= (uint8_t)(code << (((i % 64) / 32) * 4));
+      }
+    }
+    for (int j = 0; j < 4; j++) {
+      o[4 + j] = (uint8_t)((sc[j] & 0x3F) | ((sc[4 + j] >> 4) << 6));
+      o[8 + j] = (uint8_t)((mn[j] & 0x3F) | ((mn[4 + j] >> 4) << 6));
+      o[12 + j] = (uint8_t)((sc[4 + j] & 0x0F) | ((mn[4 + j] & 0x0F) << 4));
+    }
+  }
+}
+
+int encode_quant(int qtype, const float* x, int64_t n, void* out, hipStream_t s) {
+  if (qtype == SMHIP_QTYPE_Q8_0) {
+    SMHIP_REQUIRE(n % 32 == 0, "Q8_0 encode: length must be a multiple of 32");
+    hipLaunchKernelGGL(encode_q8_0_kernel, dim3(gridn(n / 32)), dim3(256), 0, s, x, (uint8_t*)out, n / 32);
+  } else if (qtype == SMHIP_QTYPE_Q4_K) {
+    SMHIP_REQUIRE(n % 256 == 0, "Q4_K encode: length must be a multiple of 256");
+    hipLaunchKernelGGL(encode_q4k_kernel, dim3(gridn(n / 256, 64)), dim3(64), 0, s, x, (uint8_t*)out, n / 256);
+  } else {
+    return fail(SMHIP_EUNSUPPORTED, "encode: qtype must be Q8_0 (8) or Q4_K (12)");
+  }
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
+}  // namespace smhip
+
+namespace smhip {
+__global__ void zero_kernel(uint32_t* __restrict__ x, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) x[i] = 0u;
+}
+// Graph-capture-safe clear (a kernel, not a memset node).  bytes must be a multiple of 4.
+int zero_bytes(void* p, size_t bytes, hipStream_t s) {
+  if (!bytes) return SMHIP_OK;
+  const int64_t n = (int64_t)(bytes / 4);
+  hipLaunchKernelGGL(zero_kernel, dim3(gridn(n)), dim3(256), 0, s, (uint32_t*)p, n);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+}  // namespace smhip

@@ -1,0 +1,453 @@
+// flash.hip — causal GQA attention on bf16 MFMA for gfx950, forward and backward.
+//
+// Same mathematics as the reference's recorded-probabilities path
+// (BackpropEngine.cs:237-388 forward, GradientKernels.Attention_Scalar
+// GradientKernels.cs:408-481 backward), restructured so that S x S
+// probabilities are never stored: the forward keeps a running (max, sum) per
+// query and saves only log-sum-exp; the backward recomputes P from it.
+//
+// All products use v_mfma_f32_32x32x16_bf16 (fp32 accumulate).  Each wave64
+// owns 32 query (or key) columns.  Scores are computed transposed where that
+// puts one query per lane, so row statistics are lane-local plus one
+// xor-32 shuffle, and the probability tile feeds the next MFMA straight from
+// registers: a lane's 16 accumulator rows are exactly the 8+8 keys it must
+// supply as the k-slice of the next product, and the matching V/K/Q/dO
+// operand is read from a transposed LDS tile with two 8-byte loads.
+//
+// Backward is deterministic: dK/dV are accumulated per (key block, query head)
+// by one workgroup and summed over the GQA group in a fixed order; dQ is a
+// separate pass over key blocks (no atomics).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace smhip {
+
+static constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ inline floatx16 mfma16(const bf16x8& a, const bf16x8& b, const floatx16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ inline void zero16(floatx16& a) {
+#pragma unroll
+  for (int e = 0; e < 16; e++) a[e] = 0.f;
+}
+__device__ inline bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
+// accumulator row of element e for this lane (32x32 MFMA output layout)
+__device__ inline int acc_row(int e, int lane) { return (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3); }
+
+// 8 accumulator values (e0..e0+7) -> bf16x8 operand (keys/queries in the lane's k-slice order)
+__device__ inline bf16x8 pack8(const floatx16& a, int e0) {
+  uint4 u;
+  u.x = pack_bf2(a[e0 + 0], a[e0 + 1]);
+  u.y = pack_bf2(a[e0 + 2], a[e0 + 3]);
+  u.z = pack_bf2(a[e0 + 4], a[e0 + 5]);
+  u.w = pack_bf2(a[e0 + 6], a[e0 + 7]);
+  return as_bf16x8(u);
+}
+// operand from a transposed LDS tile row: keys c16 + half*4 + {0..3} and c16 + 8 + half*4 + {0..3}
+__device__ inline bf16x8 tload(const uint16_t* row, int c16, int lane) {
+  const uint16_t* p = row + c16 + (lane >> 5) * 4;
+  uint2 lo = *reinterpret_cast<const uint2*>(p);
+  uint2 hi = *reinterpret_cast<const uint2*>(p + 8);
+  return as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+}
+
+// Stage rows [r0, r0+NR) x D of a bf16 matrix into LDS as [NR][D+8] and/or transposed [D][NR+8].
+template <int D, int NR, bool ROWS, bool TRANS>
+__device__ inline void stage(const uint16_t* __restrict__ g, int64_t ld, int r0, uint16_t* sRow,
+                             uint16_t* sT) {
+  constexpr int RP = D + 8, TP = NR + 8;
+  if constexpr (ROWS) {
+    for (int c = threadIdx.x; c < NR * D / 8; c += 256) {
+      const int r = c / (D / 8), dc = (c % (D / 8)) * 8;
+      *reinterpret_cast<uint4*>(sRow + r * RP + dc) = *reinterpret_cast<const uint4*>(g + (int64_t)(r0 + r) * ld + dc);
+    }
+  }
+  if constexpr (TRANS) {
+    for (int c = threadIdx.x; c < (NR / 2) * (D / 8); c += 256) {
+      const int rp = c % (NR / 2), dc = (c / (NR / 2)) * 8;
+      uint4 a = *reinterpret_cast<const uint4*>(g + (int64_t)(r0 + 2 * rp) * ld + dc);
+      uint4 b = *reinterpret_cast<const uint4*>(g + (int64_t)(r0 + 2 * rp + 1) * ld + dc);
+      const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        uint32_t lo = (j & 1) ? (av[j >> 1] >> 16) : (av[j >> 1] & 0xFFFFu);
+        uint32_t hi = (j & 1) ? (bv[j >> 1] >> 16) : (bv[j >> 1] & 0xFFFFu);
+        *reinterpret_cast<uint32_t*>(sT + (dc + j) * TP + 2 * rp) = lo | (hi << 16);
+      }
+    }
+  }
+}
+
+// ============================================================================
+// forward: grid (S/128, Hq, B), 4 waves x 32 queries, key tiles of 64
+// ============================================================================
+template <int D>
+__global__ __launch_bounds__(256) void fa_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                                     const uint16_t* __restrict__ v, uint16_t* __restrict__ o,
+                                                     float* __restrict__ lse, int S, int Hq, int Hkv, int64_t ldq,
+                                                     int64_t ldk, int64_t ldv, int64_t ldo, float sl2) {
+  constexpr int KB = 64, KP = D + 8, VP = KB + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t sK[KB * KP];
+  __shared__ __attribute__((aligned(16))) uint16_t sVt[D * VP];
+  const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest causal rows first
+  const int h = blockIdx.y, b = blockIdx.z, kvh = h / (Hq / Hkv);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int qi = qb * 128 + w * 32 + (lane & 31);
+  const uint16_t* kb = k + (int64_t)b * S * ldk + kvh * D;
+  const uint16_t* vb = v + (int64_t)b * S * ldv + kvh * D;
+
+  bf16x8 qf[D / 16];
+  {
+    const uint16_t* qrow = q + ((int64_t)b * S + qi) * ldq + h * D + (lane >> 5) * 8;
+#pragma unroll
+    for (int kk = 0; kk < D / 16; kk++) qf[kk] = as_bf16x8(*reinterpret_cast<const uint4*>(qrow + kk * 16));
+  }
+  floatx16 oacc[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; i++) zero16(oacc[i]);
+  float m = -INFINITY, l = 0.f;
+  const int kend = (qb + 1) * 128;
+  const int wq_last = qb * 128 + w * 32 + 31;  // last query of this wave
+
+  for (int k0 = 0; k0 < kend; k0 += KB) {
+    __syncthreads();
+    stage<D, KB, true, false>(kb, ldk, k0, sK, nullptr);
+    stage<D, KB, false, true>(vb, ldv, k0, nullptr, sVt);
+    __syncthreads();
+    if (k0 > wq_last) continue;  // whole tile masked for this wave
+    floatx16 sacc[2];
+    zero16(sacc[0]);
+    zero16(sacc[1]);
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int kk = 0; kk < D / 16; kk++) {
+        bf16x8 kf = as_bf16x8(*reinterpret_cast<const uint4*>(sK + (j * 32 + (lane & 31)) * KP + kk * 16 + (lane >> 5) * 8));
+        sacc[j] = mfma16(kf, qf[kk], sacc[j]);
+      }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int key = k0 + j * 32 + acc_row(e, lane);
+        float s = key <= qi ? sacc[j][e] * sl2 : -INFINITY;
+        sacc[j][e] = s;
+        mx = fmaxf(mx, s);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mnew = fmaxf(m, mx);
+    const float alpha = exp2f(m - mnew);
+    float rs = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        float p = exp2f(sacc[j][e] - mnew);
+        sacc[j][e] = p;
+        rs += p;
+      }
+    rs += __shfl_xor(rs, 32, 64);
+    l = l * alpha + rs;
+    m = mnew;
+#pragma unroll
+    for (int i = 0; i < D / 32; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) oacc[i][e] *= alpha;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const bf16x8 pf = pack8(sacc[c >> 1], 8 * (c & 1));
+#pragma unroll
+      for (int i = 0; i < D / 32; i++) {
+        const bf16x8 vf = tload(sVt + (i * 32 + (lane & 31)) * VP, c * 16, lane);
+        oacc[i] = mfma16(vf, pf, oacc[i]);
+      }
+    }
+  }
+  const float inv = 1.f / l;
+  uint16_t* orow = o + ((int64_t)b * S + qi) * ldo + h * D;
+#pragma unroll
+  for (int i = 0; i < D / 32; i++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const int d = i * 32 + g * 8 + (lane >> 5) * 4;
+      uint2 st;
+      st.x = pack_bf2(oacc[i][4 * g] * inv, oacc[i][4 * g + 1] * inv);
+      st.y = pack_bf2(oacc[i][4 * g + 2] * inv, oacc[i][4 * g + 3] * inv);
+      *reinterpret_cast<uint2*>(orow + d) = st;
+    }
+  if (lane < 32) lse[((int64_t)b * Hq + h) * S + qi] = m + log2f(l);
+}
+
+// ============================================================================
+// backward preprocessing: Di = sum_d dO*O per (b, h, q)  (the rowsum(P*dP) term)
+// ============================================================================
+template <int D>
+__global__ __launch_bounds__(256) void fa_bwd_pre_kernel(const uint16_t* __restrict__ o, const uint16_t* __restrict__ dO,
+                                                         float* __restrict__ Di, int B, int S, int Hq, int64_t ldo,
+                                                         int64_t lddo) {
+  const int lane = threadIdx.x & 63;
+  const int64_t rows = (int64_t)B * Hq * S;
+  for (int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += (int64_t)gridDim.x * 4) {
+    const int qi = (int)(r % S);
+    const int h = (int)((r / S) % Hq);
+    const int b = (int)(r / ((int64_t)S * Hq));
+    const uint16_t* orow = o + ((int64_t)b * S + qi) * ldo + h * D;
+    const uint16_t* drow = dO + ((int64_t)b * S + qi) * lddo + h * D;
+    float a = 0.f;
+    for (int d = lane; d < D; d += 64) a += bf2f(orow[d]) * bf2f(drow[d]);
+    a = wave_sum(a);
+    if (lane == 0) Di[((int64_t)b * Hq + h) * S + qi] = a;
+  }
+}
+
+// ============================================================================
+// backward dK, dV: grid (S/128, Hq, B); 4 waves x 32 keys; query tiles of 32.
+// Writes per-query-head partials dKh/dVh [B, S, Hq, D] fp32.
+// ============================================================================
+template <int D>
+__global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
+    float* __restrict__ dKh, float* __restrict__ dVh, int S, int Hq, int Hkv, int64_t ldq, int64_t ldk,
+    int64_t ldv, int64_t lddo, float sl2, float scale) {
+  constexpr int QB = 32, RP = D + 8, TP = QB + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t sQ[QB * RP];
+  __shared__ __attribute__((aligned(16))) uint16_t sQt[D * TP];
+  __shared__ __attribute__((aligned(16))) uint16_t sdO[QB * RP];
+  __shared__ __attribute__((aligned(16))) uint16_t sdOt[D * TP];
+  __shared__ float sL[QB], sDi[QB];
+  const int kbk = blockIdx.x;  // key block of 128
+  const int h = blockIdx.y, b = blockIdx.z, kvh = h / (Hq / Hkv);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int kw0 = kbk * 128 + w * 32;
+  const int kj = kw0 + (lane & 31);  // this lane's key (B-operand column)
+
+  bf16x8 kf[D / 16], vf[D / 16];
+  {
+    const uint16_t* krow = k + ((int64_t)b * S + kj) * ldk + kvh * D + (lane >> 5) * 8;
+    const uint16_t* vrow = v + ((int64_t)b * S + kj) * ldv + kvh * D + (lane >> 5) * 8;
+#pragma unroll
+    for (int kk = 0; kk < D / 16; kk++) {
+      kf[kk] = as_bf16x8(*reinterpret_cast<const uint4*>(krow + kk * 16));
+      vf[kk] = as_bf16x8(*reinterpret_cast<const uint4*>(vrow + kk * 16));
+    }
+  }
+  floatx16 dv[D / 32], dk[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; i++) { zero16(dv[i]); zero16(dk[i]); }
+  const uint16_t* qb_ = q + (int64_t)b * S * ldq + h * D;
+  const uint16_t* db_ = dO + (int64_t)b * S * lddo + h * D;
+  const float* lrow = lse + ((int64_t)b * Hq + h) * S;
+  const float* drow = Di + ((int64_t)b * Hq + h) * S;
+
+  for (int q0 = kbk * 128; q0 < S; q0 += QB) {
+    __syncthreads();
+    stage<D, QB, true, true>(qb_, ldq, q0, sQ, sQt);
+    stage<D, QB, true, true>(db_, lddo, q0, sdO, sdOt);
+    if (threadIdx.x < QB) { sL[threadIdx.x] = lrow[q0 + threadIdx.x]; sDi[threadIdx.x] = drow[q0 + threadIdx.x]; }
+    __syncthreads();
+    if (q0 + QB - 1 < kw0) continue;  // every query precedes this wave's keys
+    // S = Q K^T and dP = dO V^T : rows = queries, cols = keys (lane <-> key)
+    floatx16 sacc, dpacc;
+    zero16(sacc);
+    zero16(dpacc);
+#pragma unroll
+    for (int kk = 0; kk < D / 16; kk++) {
+      const int off = (lane & 31) * RP + kk * 16 + (lane >> 5) * 8;
+      sacc = mfma16(as_bf16x8(*reinterpret_cast<const uint4*>(sQ + off)), kf[kk], sacc);
+      dpacc = mfma16(as_bf16x8(*reinterpret_cast<const uint4*>(sdO + off)), vf[kk], dpacc);
+    }
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      const int r = acc_row(e, lane);
+      const int qi = q0 + r;
+      float p = qi >= kj ? exp2f(sacc[e] * sl2 - sL[r]) : 0.f;
+      sacc[e] = p;
+      dpacc[e] = p * (dpacc[e] - sDi[r]);  // dS
+    }
+    // dV += P^T dO ; dK += dS^T Q   (A from registers: lane row = key, k-slice = its 8+8 queries)
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const bf16x8 pf = pack8(sacc, 8 * c);
+      const bf16x8 sf = pack8(dpacc, 8 * c);
+#pragma unroll
+      for (int i = 0; i < D / 32; i++) {
+        dv[i] = mfma16(pf, tload(sdOt + (i * 32 + (lane & 31)) * TP, c * 16, lane), dv[i]);
+        dk[i] = mfma16(sf, tload(sQt + (i * 32 + (lane & 31)) * TP, c * 16, lane), dk[i]);
+      }
+    }
+  }
+  // outputs: rows = keys (acc_row), cols = d (lane)
+#pragma unroll
+  for (int i = 0; i < D / 32; i++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      const int key = kw0 + acc_row(e, lane);
+      const int64_t off = (((int64_t)b * S + key) * Hq + h) * D + i * 32 + (lane & 31);
+      dKh[off] = dk[i][e] * scale;
+      dVh[off] = dv[i][e];
+    }
+}
+
+// ============================================================================
+// backward dQ: grid (S/128, Hq, B); 4 waves x 32 queries; key tiles of 64
+// ============================================================================
+template <int D>
+__global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
+    float* __restrict__ dq, int S, int Hq, int Hkv, int64_t ldq, int64_t ldk, int64_t ldv, int64_t lddo,
+    int64_t lddq, float sl2, float scale) {
+  constexpr int KB = 64, RP = D + 8, TP = KB + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t sK[KB * RP];
+  __shared__ __attribute__((aligned(16))) uint16_t sKt[D * TP];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[KB * RP];
+  const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;
+  const int h = blockIdx.y, b = blockIdx.z, kvh = h / (Hq / Hkv);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int qi = qb * 128 + w * 32 + (lane & 31);
+  bf16x8 qf[D / 16], of[D / 16];
+  {
+    const uint16_t* qrow = q + ((int64_t)b * S + qi) * ldq + h * D + (lane >> 5) * 8;
+    const uint16_t* orow = dO + ((int64_t)b * S + qi) * lddo + h * D + (lane >> 5) * 8;
+#pragma unroll
+    for (int kk = 0; kk < D / 16; kk++) {
+      qf[kk] = as_bf16x8(*reinterpret_cast<const uint4*>(qrow + kk * 16));
+      of[kk] = as_bf16x8(*reinterpret_cast<const uint4*>(orow + kk * 16));
+    }
+  }
+  const float lq = lse[((int64_t)b * Hq + h) * S + qi];
+  const float dq_i = Di[((int64_t)b * Hq + h) * S + qi];
+  floatx16 acc[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; i++) zero16(acc[i]);
+  const uint16_t* kb = k + (int64_t)b * S * ldk + kvh * D;
+  const uint16_t* vb = v + (int64_t)b * S * ldv + kvh * D;
+  const int kend = (qb + 1) * 128;
+  const int wq_last = qb * 128 + w * 32 + 31;
+  for (int k0 = 0; k0 < kend; k0 += KB) {
+    __syncthreads();
+    stage<D, KB, true, true>(kb, ldk, k0, sK, sKt);
+    stage<D, KB, true, false>(vb, ldv, k0, sV, nullptr);
+    __syncthreads();
+    if (k0 > wq_last) continue;
+    // S^T = K Q^T, dP^T = V dO^T : rows = keys, cols = queries (lane <-> query)
+    floatx16 s[2], dp[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      zero16(s[j]);
+      zero16(dp[j]);
+#pragma unroll
+      for (int kk = 0; kk < D / 16; kk++) {
+        const int off = (j * 32 + (lane & 31)) * RP + kk * 16 + (lane >> 5) * 8;
+        s[j] = mfma16(as_bf16x8(*reinterpret_cast<const uint4*>(sK + off)), qf[kk], s[j]);
+        dp[j] = mfma16(as_bf16x8(*reinterpret_cast<const uint4*>(sV + off)), of[kk], dp[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int key = k0 + j * 32 + acc_row(e, lane);
+        float p = key <= qi ? exp2f(s[j][e] * sl2 - lq) : 0.f;
+        s[j][e] = p * (dp[j][e] - dq_i);  // dS^T
+      }
+    // dQ^T += K^T dS^T : A = K^T (lane row = d), B = dS^T from registers (lane col = query)
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const bf16x8 sf = pack8(s[c >> 1], 8 * (c & 1));
+#pragma unroll
+      for (int i = 0; i < D / 32; i++) acc[i] = mfma16(tload(sKt + (i * 32 + (lane & 31)) * TP, c * 16, lane), sf, acc[i]);
+    }
+  }
+  float* qrow = dq + ((int64_t)b * S + qi) * lddq + h * D;
+#pragma unroll
+  for (int i = 0; i < D / 32; i++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const int d = i * 32 + g * 8 + (lane >> 5) * 4;
+      *reinterpret_cast<float4*>(qrow + d) = make_float4(acc[i][4 * g] * scale, acc[i][4 * g + 1] * scale,
+                                                         acc[i][4 * g + 2] * scale, acc[i][4 * g + 3] * scale);
+    }
+}
+
+// dK/dV [b, s, kvh, :] = sum over the group's query heads (ascending) of the per-head partials.
+template <int D>
+__global__ __launch_bounds__(256) void fa_group_reduce_kernel(const float* __restrict__ dKh, const float* __restrict__ dVh,
+                                                              float* __restrict__ dk, float* __restrict__ dv, int B,
+                                                              int S, int Hq, int Hkv, int64_t lddk, int64_t lddv) {
+  const int grp = Hq / Hkv;
+  const int64_t n = (int64_t)B * S * Hkv * D;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int d = (int)(i % D);
+    const int kvh = (int)((i / D) % Hkv);
+    const int64_t t = i / ((int64_t)D * Hkv);
+    float a = 0.f, c = 0.f;
+    for (int g = 0; g < grp; g++) {
+      const int64_t off = (t * Hq + kvh * grp + g) * D + d;
+      a += dKh[off];
+      c += dVh[off];
+    }
+    dk[t * lddk + kvh * D + d] = a;
+    dv[t * lddv + kvh * D + d] = c;
+  }
+}
+
+// ---------------------------------------------------------------- launchers
+int flash_forward(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, float* lse, int B,
+                  int S, int Hq, int Hkv, int D, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
+                  hipStream_t s) {
+  SMHIP_REQUIRE(S % 128 == 0, "flash attention: S must be a multiple of 128");
+  SMHIP_REQUIRE(Hkv > 0 && Hq % Hkv == 0, "flash attention: Hq must be a multiple of Hkv");
+  const float sl2 = kLog2e / sqrtf((float)D);
+  dim3 grid(S / 128, Hq, B);
+  const int ev0 = prof_mark(s);
+  if (D == 128) hipLaunchKernelGGL(fa_fwd_kernel<128>, grid, dim3(256), 0, s, q, k, v, o, lse, S, Hq, Hkv, ldq, ldk, ldv, ldo, sl2);
+  else if (D == 64) hipLaunchKernelGGL(fa_fwd_kernel<64>, grid, dim3(256), 0, s, q, k, v, o, lse, S, Hq, Hkv, ldq, ldk, ldv, ldo, sl2);
+  else return fail(SMHIP_EUNSUPPORTED, "flash attention: head_dim must be 64 or 128");
+  SMHIP_CHECK_LAUNCH();
+  // causal: QK^T and PV over the lower triangle
+  prof_add(PROF_FLASH_FWD, ev0, prof_mark(s), 2.0 * B * Hq * (double)S * S * D);
+  return SMHIP_OK;
+}
+
+size_t flash_backward_workspace(int B, int S, int Hq, int D) {
+  return sizeof(float) * ((size_t)B * Hq * S + 2 * (size_t)B * S * Hq * D) + 256;
+}
+
+int flash_backward(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
+                   const uint16_t* dO, const float* lse, float* dq, float* dk, float* dv, int B, int S,
+                   int Hq, int Hkv, int D, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, int64_t lddo,
+                   int64_t lddq, int64_t lddk, int64_t lddv, void* ws, hipStream_t s) {
+  SMHIP_REQUIRE(S % 128 == 0, "flash attention: S must be a multiple of 128");
+  SMHIP_REQUIRE(Hkv > 0 && Hq % Hkv == 0, "flash attention: Hq must be a multiple of Hkv");
+  const float scale = 1.f / sqrtf((float)D), sl2 = kLog2e * scale;
+  float* Di = (float*)ws;
+  float* dKh = Di + (size_t)B * Hq * S;
+  float* dVh = dKh + (size_t)B * S * Hq * D;
+  const int64_t rows = (int64_t)B * Hq * S;
+  const int gpre = (int)std::min<int64_t>((rows + 3) / 4, (int64_t)num_cus() * 8);
+  const int gred = (int)std::min<int64_t>(((int64_t)B * S * Hkv * D + 255) / 256, (int64_t)num_cus() * 8);
+  dim3 grid(S / 128, Hq, B);
+  const int ev0 = prof_mark(s);
+#define FA_BWD(DD)                                                                                              \
+  hipLaunchKernelGGL(fa_bwd_pre_kernel<DD>, dim3(gpre), dim3(256), 0, s, o, dO, Di, B, S, Hq, ldo, lddo);      \
+  hipLaunchKernelGGL(fa_bwd_dkdv_kernel<DD>, grid, dim3(256), 0, s, q, k, v, dO, lse, Di, dKh, dVh, S, Hq, Hkv, \
+                     ldq, ldk, ldv, lddo, sl2, scale);                                                          \
+  hipLaunchKernelGGL(fa_bwd_dq_kernel<DD>, grid, dim3(256), 0, s, q, k, v, dO, lse, Di, dq, S, Hq, Hkv, ldq,   \
+                     ldk, ldv, lddo, lddq, sl2, scale);                                                         \
+  hipLaunchKernelGGL(fa_group_reduce_kernel<DD>, dim3(gred), dim3(256), 0, s, dKh, dVh, dk, dv, B, S, Hq, Hkv,  \
+                     lddk, lddv);
+  if (D == 128) { FA_BWD(128) }
+  else if (D == 64) { FA_BWD(64) }
+  else return fail(SMHIP_EUNSUPPORTED, "flash attention: head_dim must be 64 or 128");
+#undef FA_BWD
+  SMHIP_CHECK_LAUNCH();
+  // causal backward, algorithmic: recompute QK^T, dP = dO V^T, dV, dK, dQ (5 half-triangle products)
+  prof_add(PROF_FLASH_BWD, ev0, prof_mark(s), 5.0 * B * Hq * (double)S * S * D);
+  return SMHIP_OK;
+}
+
+}  // namespace smhip

@@ -234,7 +234,8 @@ template <int PREC, bool C_BF16>
 __global__ __launch_bounds__(NT) void gemm_kernel(OpDev A, OpDev B, OpDev A2, OpDev B2, int M, int N,
                                                   int nk1, int nk2, float alpha, float beta,
                                                   void* __restrict__ Cp, int64_t ldc, int tiles_per_split,
-                                                  float* __restrict__ partial) {
+                                                  float* __restrict__ partial, const float* __restrict__ bias,
+                                                  const float* __restrict__ R, int64_t ldr) {
   using C = TileCfg<PREC>;
   using T = typename C::T;
   __shared__ __attribute__((aligned(16))) T lds[2][2][BM * C::PK];  // [buf][A/B]
@@ -333,11 +334,14 @@ __global__ __launch_bounds__(NT) void gemm_kernel(OpDev A, OpDev B, OpDev A2, Op
         } else if constexpr (C_BF16) {
           uint16_t* Cb = (uint16_t*)Cp + (int64_t)row * ldc + col;
           float o = alpha * val;
+          if (bias) o = o + bias[col];
           if (beta != 0.f) o = o + beta * bf2f(*Cb);
           *Cb = f2bf(o);
         } else {
           float* Cf = (float*)Cp + (int64_t)row * ldc + col;
           float o = alpha * val;
+          if (bias) o = o + bias[col];
+          if (R) o = o + R[(int64_t)row * ldr + col];
           if (beta != 0.f) o = o + beta * *Cf;
           *Cf = o;
         }
@@ -348,13 +352,16 @@ __global__ __launch_bounds__(NT) void gemm_kernel(OpDev A, OpDev B, OpDev A2, Op
 // split-K: C = alpha * sum_s partial[s] + beta * C, splits summed in order.
 __global__ void splitk_reduce_kernel(const float* __restrict__ partial, int splits, int M, int N,
                                      float alpha, float beta, void* __restrict__ Cp, int64_t ldc,
-                                     int c_bf16) {
+                                     int c_bf16, const float* __restrict__ bias, const float* __restrict__ R,
+                                     int64_t ldr) {
   const int64_t n = (int64_t)M * N;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     float s = 0.f;
     for (int k = 0; k < splits; k++) s += partial[(int64_t)k * n + i];
     const int64_t row = i / N, col = i - row * N;
     float o = alpha * s;
+    if (bias) o = o + bias[col];
+    if (R && !c_bf16) o = o + R[row * ldr + col];
     if (c_bf16) {
       uint16_t* c = (uint16_t*)Cp + row * ldc + col;
       if (beta != 0.f) o = o + beta * bf2f(*c);
@@ -389,6 +396,7 @@ static OpDev make_op(const Operand& o, int R, int K, float mult) {
 
 int gemm(const GemmArgs& g, hipStream_t s) {
   if (g.M <= 0 || g.N <= 0) return SMHIP_OK;
+  SMHIP_REQUIRE(!(g.R && g.c_bf16), "gemm: residual input needs fp32 output");
   SMHIP_REQUIRE(g.precision == SMHIP_PREC_FP32 || g.precision == SMHIP_PREC_BF16, "gemm: bad precision");
   const int BK = g.precision == SMHIP_PREC_BF16 ? TileCfg<SMHIP_PREC_BF16>::BK : TileCfg<SMHIP_PREC_FP32>::BK;
   for (const Operand* o : {&g.A, &g.B}) {
@@ -415,19 +423,21 @@ int gemm(const GemmArgs& g, hipStream_t s) {
     if (!partial) return fail(SMHIP_ENOMEM, "gemm: split-K workspace");
   }
   dim3 grid(ceil_div(g.N, BN), ceil_div(g.M, BM), splits);
+  const int ev0 = prof_mark(s);
   if (g.precision == SMHIP_PREC_BF16) {
     if (g.c_bf16)
-      hipLaunchKernelGGL((gemm_kernel<SMHIP_PREC_BF16, true>), grid, dim3(NT), 0, s, A, B, A2, B2, g.M, g.N, nk1, nk2, g.alpha, g.beta, g.C, g.ldc, per, partial);
+      hipLaunchKernelGGL((gemm_kernel<SMHIP_PREC_BF16, true>), grid, dim3(NT), 0, s, A, B, A2, B2, g.M, g.N, nk1, nk2, g.alpha, g.beta, g.C, g.ldc, per, partial, g.bias, g.R, g.ldr);
     else
-      hipLaunchKernelGGL((gemm_kernel<SMHIP_PREC_BF16, false>), grid, dim3(NT), 0, s, A, B, A2, B2, g.M, g.N, nk1, nk2, g.alpha, g.beta, g.C, g.ldc, per, partial);
+      hipLaunchKernelGGL((gemm_kernel<SMHIP_PREC_BF16, false>), grid, dim3(NT), 0, s, A, B, A2, B2, g.M, g.N, nk1, nk2, g.alpha, g.beta, g.C, g.ldc, per, partial, g.bias, g.R, g.ldr);
   } else {
     SMHIP_REQUIRE(!g.c_bf16, "gemm: fp32 mode writes fp32 output");
-    hipLaunchKernelGGL((gemm_kernel<SMHIP_PREC_FP32, false>), grid, dim3(NT), 0, s, A, B, A2, B2, g.M, g.N, nk1, nk2, g.alpha, g.beta, g.C, g.ldc, per, partial);
+    hipLaunchKernelGGL((gemm_kernel<SMHIP_PREC_FP32, false>), grid, dim3(NT), 0, s, A, B, A2, B2, g.M, g.N, nk1, nk2, g.alpha, g.beta, g.C, g.ldc, per, partial, g.bias, g.R, g.ldr);
   }
   SMHIP_CHECK_LAUNCH();
+  prof_add(PROF_GEMM, ev0, prof_mark(s), 2.0 * g.M * g.N * ((double)g.K + g.K2));
   if (splits > 1) {
     int blocks = (int)std::min<int64_t>(((int64_t)g.M * g.N + 255) / 256, (int64_t)num_cus() * 8);
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, partial, splits, g.M, g.N, g.alpha, g.beta, g.C, g.ldc, g.c_bf16);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, partial, splits, g.M, g.N, g.alpha, g.beta, g.C, g.ldc, g.c_bf16, g.bias, g.R, g.ldr);
     SMHIP_CHECK_LAUNCH();
   }
   return SMHIP_OK;

@@ -41,6 +41,7 @@ int colsum_add(const float* dY, float* db, int B, int Out, hipStream_t s);
 int dequant_raw(int qtype, const void* raw, float* out, int64_t n, hipStream_t s);
 size_t planes_bytes(int qtype, int64_t n, size_t* qs_bytes);
 int repack_planes(int qtype, const void* raw, int64_t n, void* dst, QuantPlanes* out, hipStream_t s);
+int dequant_rows(const QuantPlanes& q, const int32_t* ids, float* out, int T, int D, hipStream_t s);
 
 // attention.hip
 int attention_slot_backward(const float* dO, const float* q, const float* k, const float* v,
@@ -49,4 +50,38 @@ int attention_slot_backward(const float* dO, const float* q, const float* k, con
 int attention_forward_probs(const float* q, const float* k, const float* v, float* probs, float* out,
                             int B, int S, int Hq, int Hkv, int D, hipStream_t s);
 
+}  // namespace smhip
+
+namespace smhip {
+// flash.hip
+int flash_forward(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, float* lse, int B,
+                  int S, int Hq, int Hkv, int D, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
+                  hipStream_t s);
+size_t flash_backward_workspace(int B, int S, int Hq, int D);
+int flash_backward(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
+                   const uint16_t* dO, const float* lse, float* dq, float* dk, float* dv, int B, int S,
+                   int Hq, int Hkv, int D, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, int64_t lddo,
+                   int64_t lddq, int64_t lddk, int64_t lddv, void* ws, hipStream_t s);
+// attention.hip (probability-materialising path, head-strided)
+int attention_probs_backward(const float* dO, const float* q, const float* k, const float* v,
+                             const float* probs, float* dq, float* dk, float* dv, int B, int S, int Hq,
+                             int Hkv, int D, hipStream_t s);
+// engine_kernels.hip
+int qkv_prep_forward(const float* qkv, void* q, void* k, void* v, float* rinv, const float* wq,
+                     const float* wk, const float* cosT, const float* sinT, int T, int S, int Hq, int Hkv,
+                     int D, int qk_norm, int neox, float eps, int bf16, hipStream_t s);
+int qkv_prep_backward(const float* dq, const float* dk, const float* dv, const float* qkv, const float* rinv,
+                      const float* wq, const float* wk, float* dwq, float* dwk, const float* cosT,
+                      const float* sinT, void* dqkv, int T, int S, int Hq, int Hkv, int D, int qk_norm,
+                      int neox, int bf16, hipStream_t s);
+int swiglu_fused_forward(const void* gu, void* act, int T, int F, int bf16, hipStream_t s);
+int swiglu_fused_backward(const float* dA, const void* gu, void* dgu, int T, int F, int bf16, hipStream_t s);
+int lora_mask(float* dB, int nr, int r, int Out, const int* col_starts_dev, int nblocks, hipStream_t s);
+int clip_grads(float* g, int64_t n, const float* norm_sq, float max_norm, hipStream_t s);
+int cast_bf16(const float* x, uint16_t* y, int64_t n, hipStream_t s);
+int fill_normal(float* x, int64_t n, uint64_t seed, float mean, float std, hipStream_t s);
+int fill_uniform(float* x, int64_t n, uint64_t seed, float lo, float hi, hipStream_t s);
+int fill_ids(int32_t* x, int64_t n, uint64_t seed, int V, hipStream_t s);
+int encode_quant(int qtype, const float* x, int64_t n, void* out, hipStream_t s);
+int zero_bytes(void* p, size_t bytes, hipStream_t s);
 }  // namespace smhip

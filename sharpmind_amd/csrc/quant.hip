@@ -136,3 +136,34 @@ int repack_planes(int qtype, const void* raw, int64_t n, void* dst, QuantPlanes*
 }
 
 }  // namespace smhip
+
+namespace smhip {
+// Gather + dequantise rows ids[t] of a quantised [rows][D] table (embedding lookup of a
+// frozen quantised embedding, EmbeddingTable.cs:87): out[t, i] = deq(E[ids[t], i]).
+__global__ void dequant_rows_kernel(QuantPlanes q, const int32_t* __restrict__ ids, float* __restrict__ out, int T,
+                                    int D) {
+  const int64_t n = (int64_t)T * D;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / D, c = i - t * D;
+    const int64_t e = (int64_t)ids[t] * D + c;
+    float v;
+    if (q.kind == SMHIP_QTYPE_Q8_0) {
+      v = (float)((const int8_t*)q.qs)[e] * q.sc[e >> 5];
+    } else {
+      const int w = (int)(e & 255);
+      const uint8_t b = ((const uint8_t*)q.qs)[(e >> 8) * 128 + (w >> 6) * 32 + (w & 31)];
+      const float sd = q.sc[2 * (e >> 5)], md = q.sc[2 * (e >> 5) + 1];
+      v = sd * (float)((b >> (((w & 63) >> 5) * 4)) & 0xF) - md;
+    }
+    out[i] = v;
+  }
+}
+int dequant_rows(const QuantPlanes& q, const int32_t* ids, float* out, int T, int D, hipStream_t s) {
+  const int64_t n = (int64_t)T * D;
+  if (!n) return SMHIP_OK;
+  int g = (int)std::min<int64_t>((n + 255) / 256, (int64_t)num_cus() * 8);
+  hipLaunchKernelGGL(dequant_rows_kernel, dim3(g), dim3(256), 0, s, q, ids, out, T, D);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+}  // namespace smhip

@@ -1,0 +1,93 @@
+"""Python handle on the resident training engine (smhip_engine_* in include/sharpmind_hip.h).
+
+Mirrors how the reference drives a step: TrainLoop.ForwardBackward
+(SharpMind.Training/TrainLoop.cs:222-243) then Gradients.ClipGlobalNorm and
+AdamW.Update (TrainLoop.cs:122-129).  Token ids / labels are device int32
+tensors; parameters and gradients are read back by name.
+"""
+import ctypes
+
+import numpy as np
+import torch
+
+from . import check, lib
+from .model import ModelConfig
+
+
+class CModelConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("n_layers", "d_model", "n_heads", "n_kv_heads", "head_dim", "ffn_dim",
+                                             "vocab", "batch", "seq")] + \
+        [("norm_eps", ctypes.c_float), ("rope_theta", ctypes.c_float), ("rope_neox", ctypes.c_int),
+         ("qk_norm", ctypes.c_int), ("base_qtype", ctypes.c_int), ("lora_rank", ctypes.c_int),
+         ("lora_alpha", ctypes.c_float), ("precision", ctypes.c_int), ("use_bias", ctypes.c_int),
+         ("lr", ctypes.c_float), ("beta1", ctypes.c_float), ("beta2", ctypes.c_float),
+         ("adam_eps", ctypes.c_float), ("weight_decay", ctypes.c_float), ("max_grad_norm", ctypes.c_float)]
+
+
+class Engine:
+    """One model + optimizer state resident on cuda:0."""
+
+    def __init__(self, cfg: ModelConfig, lr=1e-3, beta1=0.9, beta2=0.95, adam_eps=1e-8, weight_decay=0.1,
+                 max_grad_norm=1.0):
+        self.cfg = cfg
+        c = CModelConfig()
+        for name, _ in CModelConfig._fields_:
+            if hasattr(cfg, name):
+                setattr(c, name, getattr(cfg, name))
+        c.lr, c.beta1, c.beta2, c.adam_eps, c.weight_decay, c.max_grad_norm = lr, beta1, beta2, adam_eps, weight_decay, max_grad_norm
+        self._c = c
+        h = ctypes.c_void_p()
+        check(lib().smhip_engine_create(ctypes.byref(c), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().smhip_engine_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def param_count(self):
+        t, f = ctypes.c_int64(), ctypes.c_int64()
+        check(lib().smhip_engine_param_count(self.h, ctypes.byref(t), ctypes.byref(f)))
+        return t.value, f.value
+
+    def set(self, name, arr):
+        a = np.ascontiguousarray(arr)
+        check(lib().smhip_engine_set_tensor(self.h, name.encode(), a.ctypes.data, a.nbytes))
+
+    def get(self, name, shape, grad=False):
+        out = np.zeros(shape, np.float32)
+        check(lib().smhip_engine_get_tensor(self.h, name.encode(), 1 if grad else 0, out.ctypes.data, out.nbytes))
+        return out
+
+    def init_synthetic(self, seed=0):
+        check(lib().smhip_engine_init_synthetic(self.h, seed))
+
+    @staticmethod
+    def _stream():
+        return torch.cuda.current_stream().cuda_stream
+
+    def forward_backward(self, ids, labels, loss=None):
+        check(lib().smhip_engine_forward_backward(self.h, ids.data_ptr(), labels.data_ptr(),
+                                                  loss.data_ptr() if loss is not None else None, self._stream()))
+
+    def optimizer_step(self, grad_norm_sq=None):
+        check(lib().smhip_engine_optimizer_step(self.h, grad_norm_sq.data_ptr() if grad_norm_sq is not None else None,
+                                                self._stream()))
+
+    def step(self, ids, labels, loss=None):
+        check(lib().smhip_engine_step(self.h, ids.data_ptr(), labels.data_ptr(),
+                                      loss.data_ptr() if loss is not None else None, self._stream()))
+
+
+def next_token_labels(ids, seq):
+    """labels[b, s] = ids[b, s+1], -100 at the end of each sequence (CLM shift, TrainingBatch.cs:8)."""
+    lab = torch.roll(ids, -1)
+    lab = lab.view(-1, seq).clone()
+    lab[:, -1] = -100
+    return lab.view(-1).contiguous()

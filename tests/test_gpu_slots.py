@@ -272,6 +272,22 @@ def test_cross_entropy(orc, dev, Tn, V, sm):
     assert abs(float(H(loss)[0]) - rloss) <= FP32_TOL * abs(rloss)
 
 
+@pytest.mark.parametrize("Tn,V", [(64, 512), (32, 32000), (4, 151936)])
+def test_cross_entropy_in_place(orc, dev, Tn, V):
+    """dLogits written over the logits buffer (the fp32 engine does this): loss must use the original row."""
+    rng = np.random.default_rng(V)
+    z = f32(rng.standard_normal((Tn, V)) * 2)
+    lab = rng.integers(0, V, Tn).astype(np.int32)
+    lab[1] = -100
+    ref = np.zeros_like(z)
+    orc.orc_ce_softmax_grad(z, lab, ref, Tn, V, -100, 0.0)
+    rloss = orc.orc_ce_loss(z, lab, Tn, V, -100, 0.0)
+    tz = T(z, dev)
+    d, loss = hip.cross_entropy_softmax(tz, T(lab, dev), -100, 0.0, out=tz)
+    assert rel_err(H(tz), ref) <= FP32_TOL
+    assert abs(float(H(loss)[0]) - rloss) <= FP32_TOL * abs(rloss)
+
+
 # ------------------------------------------------------------------ TrainingOps
 @pytest.mark.parametrize("n", [1_000_003, 7])
 def test_adamw_bitexact(orc, dev, n):
