@@ -5,6 +5,8 @@
 // signatures on host memory: copy in, run the device entry, copy out.
 #include <hip/hip_runtime.h>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -67,7 +69,7 @@ void* workspace(hipStream_t s, size_t bytes, int slot) {
 struct Profiler {
   std::vector<hipEvent_t> ev;
   size_t used = 0;
-  struct Rec { int cat, i0, i1; double flops; };
+  struct Rec { int cat, i0, i1; double flops; int M, N, K; };
   std::vector<Rec> recs;
 };
 static thread_local Profiler* g_prof = nullptr;
@@ -78,8 +80,8 @@ int prof_mark(hipStream_t s) {
   hipEventRecord(p->ev[p->used], s);
   return (int)p->used++;
 }
-void prof_add(int cat, int i0, int i1, double flops) {
-  if (g_prof && i0 >= 0 && i1 >= 0) g_prof->recs.push_back({cat, i0, i1, flops});
+void prof_add(int cat, int i0, int i1, double flops, int M, int N, int K) {
+  if (g_prof && i0 >= 0 && i1 >= 0) g_prof->recs.push_back({cat, i0, i1, flops, M, N, K});
 }
 
 }  // namespace smhip
@@ -113,6 +115,21 @@ extern "C" int smhip_profile_end(double* out, int ncat) {
       out[3 * r.cat] += ms;
       out[3 * r.cat + 1] += 1.0;
       out[3 * r.cat + 2] += r.flops;
+    }
+  }
+  if (!rc) {
+    // optional per-launch listing for offline analysis: SMHIP_PROFILE_DUMP=<path>
+    const char* path = getenv("SMHIP_PROFILE_DUMP");
+    if (path && *path) {
+      FILE* f = fopen(path, "w");
+      if (f) {
+        for (auto& r : p->recs) {
+          float ms = 0.f;
+          hipEventElapsedTime(&ms, p->ev[r.i0], p->ev[r.i1]);
+          fprintf(f, "%d %d %d %d %.6f %.0f\n", r.cat, r.M, r.N, r.K, ms, r.flops);
+        }
+        fclose(f);
+      }
     }
   }
   for (auto& e : p->ev) hipEventDestroy(e);

@@ -396,6 +396,11 @@ static OpDev make_op(const Operand& o, int R, int K, float mult) {
 
 int gemm(const GemmArgs& g, hipStream_t s) {
   if (g.M <= 0 || g.N <= 0) return SMHIP_OK;
+  if (!g.R || !g.c_bf16) {
+    const int fast = gemm_bf16_fast(g, s);
+    if (fast < 0) return fast;
+    if (fast > 0) return SMHIP_OK;
+  }
   SMHIP_REQUIRE(!(g.R && g.c_bf16), "gemm: residual input needs fp32 output");
   SMHIP_REQUIRE(g.precision == SMHIP_PREC_FP32 || g.precision == SMHIP_PREC_BF16, "gemm: bad precision");
   const int BK = g.precision == SMHIP_PREC_BF16 ? TileCfg<SMHIP_PREC_BF16>::BK : TileCfg<SMHIP_PREC_FP32>::BK;
@@ -434,7 +439,7 @@ int gemm(const GemmArgs& g, hipStream_t s) {
     hipLaunchKernelGGL((gemm_kernel<SMHIP_PREC_FP32, false>), grid, dim3(NT), 0, s, A, B, A2, B2, g.M, g.N, nk1, nk2, g.alpha, g.beta, g.C, g.ldc, per, partial, g.bias, g.R, g.ldr);
   }
   SMHIP_CHECK_LAUNCH();
-  prof_add(PROF_GEMM, ev0, prof_mark(s), 2.0 * g.M * g.N * ((double)g.K + g.K2));
+  prof_add(PROF_GEMM, ev0, prof_mark(s), 2.0 * g.M * g.N * ((double)g.K + g.K2), g.M, g.N, g.K + g.K2);
   if (splits > 1) {
     int blocks = (int)std::min<int64_t>(((int64_t)g.M * g.N + 255) / 256, (int64_t)num_cus() * 8);
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, partial, splits, g.M, g.N, g.alpha, g.beta, g.C, g.ldc, g.c_bf16, g.bias, g.R, g.ldr);

@@ -37,6 +37,9 @@ int add_inplace(float* y, const float* x, int64_t n, hipStream_t s);
 int f32_to_bf16(const float* x, uint16_t* y, int64_t n, hipStream_t s);
 int colsum_add(const float* dY, float* db, int B, int Out, hipStream_t s);
 
+// gemm_bf16.hip: 1 = ran, 0 = not eligible (generic kernel), <0 = error
+int gemm_bf16_fast(const GemmArgs& g, hipStream_t s);
+
 // quant.hip
 int dequant_raw(int qtype, const void* raw, float* out, int64_t n, hipStream_t s);
 size_t planes_bytes(int qtype, int64_t n, size_t* qs_bytes);
