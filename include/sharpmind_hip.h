@@ -155,6 +155,14 @@ int smhip_flash_attention_backward(const void* q, const void* k, const void* v, 
                                    int64_t ldv, int64_t ldo, int64_t lddo, int64_t lddq,
                                    int64_t lddk, int64_t lddv, smhip_stream_t stream);
 
+/* General dense GEMM on MFMA: C[M,N] = alpha * sum_k A(m,k) B(n,k) + beta * C.
+ * Operand modes: 0 fp32 k-contiguous (X[r*ld + k]), 1 fp32 row-contiguous (X[k*ld + r]),
+ * 2 bf16 k-contiguous, 3 bf16 row-contiguous.  C is fp32 (c_bf16 = 0) or bf16.  split_k > 1 splits
+ * the reduction deterministically.  precision: SMHIP_PREC_FP32 (fp32 MFMA) or SMHIP_PREC_BF16. */
+int smhip_gemm(int M, int N, int K, int a_mode, const void* A, int64_t lda, int b_mode, const void* B,
+               int64_t ldb, float alpha, float beta, void* C, int64_t ldc, int c_bf16, int split_k,
+               int precision, smhip_stream_t stream);
+
 /* TensorQuantizer.Quantize for Q8_0 / Q4_K on the device (TensorQuantizer.cs:80-144,
  * TensorQuantizer.KQuant.cs:173-225): same bytes as the reference encoder. */
 int smhip_quantize(int qtype, const float* x, int64_t n, void* out, smhip_stream_t stream);

@@ -527,6 +527,23 @@ int smhip_host_qmatmul(int qtype, const float* in, const void* rawW, float* out,
 
 extern "C" {
 
+int smhip_gemm(int M, int N, int K, int a_mode, const void* A, int64_t lda, int b_mode, const void* B, int64_t ldb,
+               float alpha, float beta, void* C, int64_t ldc, int c_bf16, int split_k, int precision,
+               smhip_stream_t stream) {
+  SMHIP_REQUIRE(M >= 0 && N >= 0 && K > 0 && A && B && C, "gemm: bad arguments");
+  SMHIP_REQUIRE(a_mode >= 0 && a_mode <= 3 && b_mode >= 0 && b_mode <= 3, "gemm: operand modes must be 0..3");
+  SMHIP_REQUIRE(beta == 0.f || beta == 1.f, "gemm: beta must be 0 or 1");
+  GemmArgs g{};
+  g.M = M; g.N = N; g.K = K;
+  g.A = {a_mode, A, nullptr, lda};
+  g.B = {b_mode, B, nullptr, ldb};
+  g.alpha = alpha; g.beta = beta;
+  g.C = C; g.ldc = ldc; g.c_bf16 = c_bf16;
+  g.precision = precision;
+  g.split_k = split_k > 0 ? split_k : 1;
+  return gemm(g, STREAM(stream));
+}
+
 int smhip_flash_attention_forward(const void* q, const void* k, const void* v, void* o, float* lse, int B, int S,
                                   int Hq, int Hkv, int D, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
                                   smhip_stream_t stream) {

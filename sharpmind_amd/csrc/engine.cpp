@@ -125,8 +125,8 @@ static int build(Engine* e) {
         add(&w.w[p], (int64_t)e->Out[p] * e->In[p], true, true, true);
         if (c.use_bias) add(&w.b[p], e->Out[p], true, false, false);
       } else {
-        add(&w.la[p], (int64_t)e->In[p] * e->nr[p], true, true, false);
-        add(&w.lb[p], (int64_t)e->nr[p] * e->Out[p], true, true, false);
+        add(&w.la[p], (int64_t)e->In[p] * e->nr[p], true, true, true);
+        add(&w.lb[p], (int64_t)e->nr[p] * e->Out[p], true, true, true);
       }
     }
   }
@@ -143,7 +143,7 @@ static int build(Engine* e) {
   e->m = (float*)dalloc(e, tb);
   e->v = (float*)dalloc(e, tb);
   if (!e->train || !e->grad || !e->m || !e->v) return fail(SMHIP_ENOMEM, "engine: parameter arena");
-  if (full && e->bf) {
+  if (e->bf) {  // bf16 GEMM operand copies of the trainable weights (full mode) or adapters (LoRA)
     e->train_bf = (uint16_t*)dalloc(e, sizeof(uint16_t) * (size_t)std::max<int64_t>(e->n_train, 1));
     if (!e->train_bf) return fail(SMHIP_ENOMEM, "engine: bf16 shadow");
   }
@@ -306,13 +306,20 @@ static Operand w_bwd(const Engine* e, const LayerW& w, int p) {
 static int prec(const Engine* e) { return e->bf ? SMHIP_PREC_BF16 : SMHIP_PREC_FP32; }
 static float lora_scale(const Engine* e) { return e->c.lora_alpha / (float)e->c.lora_rank; }
 
+// split-K factor: enough workgroups (about 2 per CU) for GEMMs whose output has few 128x128 tiles
 static int split_for(int M, int N, int K) {
   const int tiles = ceil_div(M, 128) * ceil_div(N, 128);
-  const int ks = ceil_div(K, 32);
-  if (tiles >= num_cus() || ks < 16) return 1;
-  int s = num_cus() / tiles;
-  s = std::min(s, ks / 4);
+  const int kt = K / 64;
+  if (tiles >= num_cus() || kt < 4) return 1;
+  int s = (2 * num_cus()) / tiles;
+  s = std::min(s, kt / 2);
   return std::max(1, std::min(s, 32));
+}
+
+// LoRA operand: bf16 shadow in bf16 mode, fp32 master otherwise
+static Operand lora_op(const Engine* e, const DenseRef& t, bool kmode, int64_t ld) {
+  if (e->bf && t.bf) return Operand{kmode ? SRC_BF16_K : SRC_BF16_R, t.bf, nullptr, ld};
+  return Operand{kmode ? SRC_F32_K : SRC_F32_R, t.data, nullptr, ld};
 }
 
 // y (fp32 or TA) = x W^T [+ s (x A) B] [+ bias] [+ R]
@@ -330,13 +337,13 @@ static int proj_forward(Engine* e, int l, int p, const void* x, void* y, int y_b
     u.alpha = 1.f;
     u.M = T; u.N = nr; u.K = In;
     u.A = act_k(e, x, In);
-    u.B = Operand{SRC_F32_R, w.la[p].data, nullptr, nr};
+    u.B = lora_op(e, w.la[p], false, nr);
     u.C = e->sv[l].u[p]; u.ldc = nr; u.c_bf16 = e->bf;
     u.split_k = split_for(T, nr, In);
     if (int rc = gemm(u, s)) return rc;
     g.K2 = nr;
     g.A2 = act_k(e, e->sv[l].u[p], nr);
-    g.B2 = Operand{SRC_F32_R, w.lb[p].data, nullptr, Out};
+    g.B2 = lora_op(e, w.lb[p], false, Out);
     g.alpha2 = lora_scale(e);
   }
   g.M = T; g.N = Out; g.K = In;
@@ -365,7 +372,7 @@ static int proj_backward(Engine* e, int l, int p, const void* dY, const float* d
     z.precision = prec(e); z.alpha = 1.f;
     z.M = T; z.N = nr; z.K = Out;
     z.A = act_k(e, dY, Out);
-    z.B = Operand{SRC_F32_K, w.lb[p].data, nullptr, Out};
+    z.B = lora_op(e, w.lb[p], true, Out);
     z.C = e->z; z.ldc = nr; z.c_bf16 = e->bf;
     z.split_k = split_for(T, nr, Out);
     if (int rc = gemm(z, s)) return rc;
@@ -396,7 +403,7 @@ static int proj_backward(Engine* e, int l, int p, const void* dY, const float* d
     if (int rc = gemm(ga, s)) return rc;
     g.K2 = nr;
     g.A2 = act_k(e, e->z, nr);
-    g.B2 = Operand{SRC_F32_K, w.la[p].data, nullptr, nr};
+    g.B2 = lora_op(e, w.la[p], true, nr);
     g.alpha2 = sc;
   } else {
     // dW += dY^T x   [Out, In]
@@ -690,6 +697,8 @@ int smhip_engine_set_tensor(void* engine, const char* name, const void* host, in
         SMHIP_CHECK_HIP(hipMemcpy2D(w.lb[p].data + (int64_t)blk * r * e->Out[p] + coff, sizeof(float) * e->Out[p], host,
                                     sizeof(float) * Out, sizeof(float) * Out, r, hipMemcpyHostToDevice));
       }
+      const DenseRef& t = isB ? w.lb[p] : w.la[p];
+      if (t.bf) return cast_bf16(t.data, t.bf, t.n, nullptr);
       return SMHIP_OK;
     }
   }
@@ -792,6 +801,7 @@ int smhip_engine_init_synthetic(void* engine, uint64_t seed) {
                             p == P_QKV ? 3 : 2, s)))
           return rc;
     }
+  if (e->train_bf && (rc = cast_bf16(e->train, e->train_bf, e->n_train, s))) return rc;
   return hipDeviceSynchronize() == hipSuccess ? SMHIP_OK : fail(SMHIP_EHIP, "init_synthetic");
 }
 

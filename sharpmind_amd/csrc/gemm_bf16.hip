@@ -264,6 +264,8 @@ struct Args {
   const float* R;
   int64_t ldr;
   int tiles_m, tiles_n;
+  int kps;          // main K tiles per split (blockIdx.y = split)
+  float* partial;   // non-null: write raw partial sums [split][M][N] instead of C
 };
 
 template <int BM, int AMODE, int BMODE, bool C_BF16>
@@ -301,8 +303,11 @@ __global__ __launch_bounds__(NT, BM == 128 ? 2 : 1) void gemm_bf16_kernel(Args g
 
   typename LoaderFor<AMODE, BM>::T la;
   typename LoaderFor<BMODE, BN>::T lb;
-  const int nk1 = g.K / BK;
-  const int nk2 = (g.K2 + BK - 1) / BK;
+  const int nk_all = g.K / BK;
+  const int split = blockIdx.y, nsplit = gridDim.y;
+  const int kt0 = split * g.kps;
+  const int nk1 = max(0, min(nk_all, kt0 + g.kps) - kt0);           // main K tiles of this split
+  const int nk2 = split == nsplit - 1 ? (g.K2 + BK - 1) / BK : 0;   // rank extension: last split only
   const int nt = nk1 + nk2;
 
   auto compute = [&](int buf) {
@@ -330,11 +335,11 @@ __global__ __launch_bounds__(NT, BM == 128 ? 2 : 1) void gemm_bf16_kernel(Args g
   };
 
   if (nk1 > 0) {
-    la.load(g.A, m0, 0, g.M);
-    lb.load(g.B, n0, 0, g.N);
+    la.load(g.A, m0, kt0 * BK, g.M);
+    lb.load(g.B, n0, kt0 * BK, g.N);
     la.store(sA[0]);
     lb.store(sB[0]);
-  } else {
+  } else if (nk2 > 0) {
     gen_tile<BM>(g.amode2, g.A2, m0, 0, g.M, g.K2, g.alpha2, sA[0]);
     gen_tile<BN>(g.bmode2, g.B2, n0, 0, g.N, g.K2, 1.f, sB[0]);
   }
@@ -343,8 +348,8 @@ __global__ __launch_bounds__(NT, BM == 128 ? 2 : 1) void gemm_bf16_kernel(Args g
     const int buf = t & 1;
     const bool next_main = t + 1 < nk1;
     if (next_main) {
-      la.load(g.A, m0, (t + 1) * BK, g.M);
-      lb.load(g.B, n0, (t + 1) * BK, g.N);
+      la.load(g.A, m0, (kt0 + t + 1) * BK, g.M);
+      lb.load(g.B, n0, (kt0 + t + 1) * BK, g.N);
     }
     compute(buf);
     if (next_main) {
@@ -370,6 +375,10 @@ __global__ __launch_bounds__(NT, BM == 128 ? 2 : 1) void gemm_bf16_kernel(Args g
       for (int e = 0; e < 16; e++) {
         const int row = m0 + wm * WM + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
         if (row >= g.M) continue;
+        if (g.partial) {
+          g.partial[((int64_t)split * g.M + row) * g.N + col] = acc[i][j][e];
+          continue;
+        }
         float o = g.alpha * acc[i][j][e] + bv;
         if constexpr (C_BF16) {
           uint16_t* c = (uint16_t*)g.C + (int64_t)row * g.ldc + col;
@@ -386,30 +395,54 @@ __global__ __launch_bounds__(NT, BM == 128 ? 2 : 1) void gemm_bf16_kernel(Args g
 }
 
 template <int BM, int AM, int BMD>
-static void launch_c(const Args& a, int c_bf16, hipStream_t s) {
-  const int ntiles = a.tiles_m * a.tiles_n;
-  if (c_bf16) hipLaunchKernelGGL((gemm_bf16_kernel<BM, AM, BMD, true>), dim3(ntiles), dim3(NT), 0, s, a);
-  else hipLaunchKernelGGL((gemm_bf16_kernel<BM, AM, BMD, false>), dim3(ntiles), dim3(NT), 0, s, a);
+static void launch_c(const Args& a, int c_bf16, int splits, hipStream_t s) {
+  const dim3 grid(a.tiles_m * a.tiles_n, splits);
+  if (c_bf16 && !a.partial) hipLaunchKernelGGL((gemm_bf16_kernel<BM, AM, BMD, true>), grid, dim3(NT), 0, s, a);
+  else hipLaunchKernelGGL((gemm_bf16_kernel<BM, AM, BMD, false>), grid, dim3(NT), 0, s, a);
 }
 
 template <int BM>
-static bool dispatch(const Args& a, int amode, int bmode, int c_bf16, hipStream_t s) {
+static bool dispatch(const Args& a, int amode, int bmode, int c_bf16, int sp, hipStream_t s) {
   if (amode == SRC_BF16_K) {
     switch (bmode) {
-      case SRC_BF16_K: launch_c<BM, SRC_BF16_K, SRC_BF16_K>(a, c_bf16, s); return true;
-      case SRC_BF16_R: launch_c<BM, SRC_BF16_K, SRC_BF16_R>(a, c_bf16, s); return true;
-      case SRC_Q8_K: launch_c<BM, SRC_BF16_K, SRC_Q8_K>(a, c_bf16, s); return true;
-      case SRC_Q8_R: launch_c<BM, SRC_BF16_K, SRC_Q8_R>(a, c_bf16, s); return true;
-      case SRC_Q4K_K: launch_c<BM, SRC_BF16_K, SRC_Q4K_K>(a, c_bf16, s); return true;
-      case SRC_Q4K_R: launch_c<BM, SRC_BF16_K, SRC_Q4K_R>(a, c_bf16, s); return true;
+      case SRC_BF16_K: launch_c<BM, SRC_BF16_K, SRC_BF16_K>(a, c_bf16, sp, s); return true;
+      case SRC_BF16_R: launch_c<BM, SRC_BF16_K, SRC_BF16_R>(a, c_bf16, sp, s); return true;
+      case SRC_Q8_K: launch_c<BM, SRC_BF16_K, SRC_Q8_K>(a, c_bf16, sp, s); return true;
+      case SRC_Q8_R: launch_c<BM, SRC_BF16_K, SRC_Q8_R>(a, c_bf16, sp, s); return true;
+      case SRC_Q4K_K: launch_c<BM, SRC_BF16_K, SRC_Q4K_K>(a, c_bf16, sp, s); return true;
+      case SRC_Q4K_R: launch_c<BM, SRC_BF16_K, SRC_Q4K_R>(a, c_bf16, sp, s); return true;
       default: return false;
     }
   }
-  if (amode == SRC_BF16_R && bmode == SRC_BF16_R && !c_bf16) {
-    launch_c<BM, SRC_BF16_R, SRC_BF16_R>(a, 0, s);
+  if (amode == SRC_BF16_R && bmode == SRC_BF16_R && (!c_bf16 || a.partial)) {
+    launch_c<BM, SRC_BF16_R, SRC_BF16_R>(a, 0, sp, s);
     return true;
   }
   return false;
+}
+
+// C = alpha * sum_s partial[s] (+ bias) (+ R) (+ beta C); splits summed in ascending order.
+__global__ void splitk_epilogue_kernel(const float* __restrict__ partial, int splits, int M, int N, float alpha,
+                                       float beta, void* __restrict__ Cp, int64_t ldc, int c_bf16,
+                                       const float* __restrict__ bias, const float* __restrict__ R, int64_t ldr) {
+  const int64_t n = (int64_t)M * N;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    float acc = 0.f;
+    for (int k = 0; k < splits; k++) acc += partial[(int64_t)k * n + i];
+    const int64_t row = i / N, col = i - row * N;
+    float o = alpha * acc;
+    if (bias) o = o + bias[col];
+    if (c_bf16) {
+      uint16_t* c = (uint16_t*)Cp + row * ldc + col;
+      if (beta != 0.f) o = o + beta * bf2f(*c);
+      *c = f2bf(o);
+    } else {
+      float* c = (float*)Cp + row * ldc + col;
+      if (R) o = o + R[row * ldr + col];
+      if (beta != 0.f) o = o + beta * *c;
+      *c = o;
+    }
+  }
 }
 
 }  // namespace g2
@@ -419,7 +452,7 @@ static bool aligned_16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // Returns 1 if the fast path ran, 0 if the shape/modes need the generic kernel, <0 on error.
 int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   using namespace g2;
-  if (g.precision != SMHIP_PREC_BF16 || g.split_k > 1) return 0;
+  if (g.precision != SMHIP_PREC_BF16) return 0;
   if (g.K % BK != 0 || g.K2 > 4 * BK) return 0;
   const int am = g.A.mode, bm = g.B.mode;
   const bool a_ok = am == SRC_BF16_K || am == SRC_BF16_R;
@@ -454,11 +487,26 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   const int t256 = ceil_div(g.M, 256) * a.tiles_n;
   const bool big = t256 >= 2 * num_cus();
   a.tiles_m = ceil_div(g.M, big ? 256 : 128);
+  const int nk = g.K / BK;
+  int sp = std::max(1, std::min(g.split_k, nk));
+  a.kps = ceil_div(nk, sp);
+  sp = ceil_div(nk, a.kps);
+  a.partial = nullptr;
+  if (sp > 1) {
+    a.partial = (float*)workspace(s, sizeof(float) * (size_t)sp * g.M * g.N, 3);
+    if (!a.partial) return fail(SMHIP_ENOMEM, "gemm: split-K workspace");
+  }
   const int ev0 = prof_mark(s);
-  const bool ok = big ? dispatch<256>(a, am, bm, g.c_bf16, s) : dispatch<128>(a, am, bm, g.c_bf16, s);
+  const bool ok = big ? dispatch<256>(a, am, bm, g.c_bf16, sp, s) : dispatch<128>(a, am, bm, g.c_bf16, sp, s);
   if (!ok) return 0;
   SMHIP_CHECK_LAUNCH();
   prof_add(PROF_GEMM, ev0, prof_mark(s), 2.0 * g.M * g.N * ((double)g.K + g.K2), g.M, g.N, g.K + g.K2);
+  if (sp > 1) {
+    const int blocks = (int)std::min<int64_t>(((int64_t)g.M * g.N + 255) / 256, (int64_t)num_cus() * 8);
+    hipLaunchKernelGGL(splitk_epilogue_kernel, dim3(blocks), dim3(256), 0, s, a.partial, sp, g.M, g.N, g.alpha,
+                       g.beta, g.C, g.ldc, g.c_bf16, g.bias, g.R, g.ldr);
+    SMHIP_CHECK_LAUNCH();
+  }
   return 1;
 }
 

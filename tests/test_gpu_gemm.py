@@ -1,0 +1,48 @@
+"""The MFMA GEMM primitive (smhip_gemm) against float64 on the same (bf16-representable) inputs.
+
+Products of bf16 values are exact in fp32 and MFMA accumulates in fp32, so the
+bar is the fp32 one (1e-5 norm-wise) for fp32 output; bf16 output adds one
+rounding (2e-2 bar, measures ~2e-3).  Shapes cover the fast kernel (K % 64 ==
+0, both tile heights, split-K, ragged M/N edges, transposed operands) and the
+generic fallback (K not a multiple of 64).
+"""
+import numpy as np
+import pytest
+import torch
+
+import sharpmind_amd
+from sharpmind_amd import check
+
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _rnd(shape, rng):
+    return torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).to(torch.bfloat16).float().numpy()
+
+
+@pytest.mark.parametrize("M,N,K,am,bm,split", [
+    (256, 256, 256, 2, 2, 1), (4096, 1024, 1024, 2, 3, 1), (300, 136, 192, 2, 3, 1), (4096, 48, 1024, 2, 3, 8),
+    (48, 1024, 4096, 3, 3, 8), (1000, 32, 2048, 3, 3, 13), (8192, 512, 128, 2, 2, 1), (130, 200, 100, 2, 2, 1),
+    (64, 64, 64, 0, 1, 1)])
+@pytest.mark.parametrize("c_bf16", [0, 1])
+def test_gemm_modes(dev, M, N, K, am, bm, split, c_bf16):
+    rng = np.random.default_rng(M + N + K + am + bm)
+    a = _rnd((M, K), rng)
+    b = _rnd((N, K), rng)
+    c0 = _rnd((M, N), rng)
+    dt = torch.bfloat16 if am >= 2 else torch.float32
+    ta = torch.from_numpy(np.ascontiguousarray(a if am % 2 == 0 else a.T)).to(dev).to(dt)
+    dtb = torch.bfloat16 if bm >= 2 else torch.float32
+    tb = torch.from_numpy(np.ascontiguousarray(b if bm % 2 == 0 else b.T)).to(dev).to(dtb)
+    lda = K if am % 2 == 0 else M
+    ldb = K if bm % 2 == 0 else N
+    for beta in (0.0, 1.0):
+        tc = torch.from_numpy(c0).to(dev).to(torch.bfloat16 if c_bf16 else torch.float32)
+        check(sharpmind_amd.lib().smhip_gemm(M, N, K, am, ta.data_ptr(), lda, bm, tb.data_ptr(), ldb, 0.5, beta,
+                                             tc.data_ptr(), N, c_bf16, split, 1, torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        ref = 0.5 * (a.astype(np.float64) @ b.astype(np.float64).T) + beta * c0
+        tol = 2e-2 if c_bf16 else 1e-5
+        assert rel_err(tc.float().cpu().numpy(), ref) <= tol, (beta, rel_err(tc.float().cpu().numpy(), ref))
