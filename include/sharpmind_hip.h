@@ -101,6 +101,16 @@ int smhip_scale_inplace(float* x, int64_t n, float scale, smhip_stream_t stream)
 int smhip_qmatmul(int qtype, const float* in, const void* rawW, float* out, int M, int K, int N,
                   int precision, smhip_stream_t stream);
 
+/* Dequant-fused bf16 MFMA GEMM through a frozen quantised weight: the forward product
+ * (trans_w = 0: C[M,N] = A[M,K] . deq(W)^T, W rows [N][K]) and the dX product of the backward
+ * (trans_w = 1: C[M,N] = A[M,K] . deq(W), W rows [K][N]; dX = dY W with K = Out, N = In).
+ * A is bf16 with row stride lda, C fp32.  The weight values are the bit-exact dequantised fp32
+ * values of the reference layout (ReadQ8_0_Scalar QuantizationKernels.Q8.cs:412-433,
+ * ReadQ4K_Scalar QuantizationKernels.Q4.cs:951-981), rounded once to bf16.  The reference has
+ * no backward through quantised weights; this is the dX half of QuantizedMatMulFn's gradient. */
+int smhip_qgemm_bf16(int qtype, int trans_w, int M, int N, int K, const void* A, int64_t lda, const void* rawW,
+                     float* C, int64_t ldc, smhip_stream_t stream);
+
 /* Bit-exact dequantisation of a reference-layout stream of n elements
  * (ReadQ8_0_Scalar QuantizationKernels.Q8.cs:412-433, ReadQ4K_Scalar QuantizationKernels.Q4.cs:951-981). */
 int smhip_dequant(int qtype, const void* raw, float* out, int64_t n, smhip_stream_t stream);

@@ -270,6 +270,40 @@ int smhip_qmatmul(int qtype, const float* in, const void* rawW, float* out, int 
   return gemm(g, s);
 }
 
+int smhip_qgemm_bf16(int qtype, int trans_w, int M, int N, int K, const void* A, int64_t lda, const void* rawW,
+                     float* C, int64_t ldc, smhip_stream_t stream) {
+  SMHIP_REQUIRE(M >= 0 && N > 0 && K > 0 && A && rawW && C, "qgemm_bf16: bad arguments");
+  SMHIP_REQUIRE(qtype == SMHIP_QTYPE_Q8_0 || qtype == SMHIP_QTYPE_Q4_K, "qgemm_bf16: qtype must be 8 (Q8_0) or 12 (Q4_K)");
+  SMHIP_REQUIRE(K % 64 == 0 && N % 32 == 0, "qgemm_bf16: K must be a multiple of 64 and N of 32");
+  hipStream_t s = STREAM(stream);
+  const int64_t n = (int64_t)N * K;
+  // W rows: [N][K] (trans_w = 0) or [K][N] (trans_w = 1); the row length must hold whole blocks
+  const int64_t row = trans_w ? N : K;
+  if (qtype == SMHIP_QTYPE_Q4_K) SMHIP_REQUIRE(row % 256 == 0, "qgemm_bf16: Q4_K rows must hold whole 256-element super-blocks");
+  void* planes = workspace(s, planes_bytes(qtype, n, nullptr), 5);
+  if (!planes) return fail(SMHIP_ENOMEM, "qgemm_bf16: workspace");
+  QuantPlanes qp;
+  if (int rc = repack_planes(qtype, rawW, n, planes, &qp, s)) return rc;
+  GemmArgs g{};
+  g.precision = SMHIP_PREC_BF16;
+  g.split_k = 1;
+  g.alpha = 1.f;
+  g.M = M; g.N = N; g.K = K;
+  g.A = {SRC_BF16_K, A, nullptr, lda};
+  g.C = C; g.ldc = ldc;
+  if (!trans_w) {
+    g.B = {qtype == SMHIP_QTYPE_Q8_0 ? SRC_Q8_K : SRC_Q4K_K, qp.qs, qp.sc, K};
+  } else {
+    void* cols = workspace(s, planes_bytes(qtype, n, nullptr), 8);
+    if (!cols) return fail(SMHIP_ENOMEM, "qgemm_bf16: workspace");
+    QuantPlanes qc;
+    if (int rc = make_col_planes(qp, K, N, cols, &qc, s)) return rc;
+    g.B = {qtype == SMHIP_QTYPE_Q8_0 ? SRC_Q8T : SRC_Q4KT, qc.qs, qc.sc, K};
+  }
+  const int rc = gemm(g, s);
+  return rc;
+}
+
 int smhip_dequant(int qtype, const void* raw, float* out, int64_t n, smhip_stream_t stream) {
   SMHIP_REQUIRE(n >= 0 && (n == 0 || (raw && out)), "dequant: bad arguments");
   return dequant_raw(qtype, raw, out, n, STREAM(stream));

@@ -40,7 +40,12 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 // float -> bf16 bits, round to nearest even (NaN kept quiet).
+// The device pass uses the hardware conversion (v_cvt_pk_bf16_f32, IEEE round to nearest
+// even); the host pass rounds the same way in software.
 __device__ __host__ inline uint16_t f2bf(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+#endif
   uint32_t u = __builtin_bit_cast(uint32_t, f);
   if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
   u += 0x7FFFu + ((u >> 16) & 1u);
@@ -50,7 +55,10 @@ __device__ __host__ inline float bf2f(uint16_t b) {
   return __builtin_bit_cast(float, (uint32_t)b << 16);
 }
 __device__ inline uint32_t pack_bf2(float lo, float hi) {
-  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+  bf16x2 v;
+  v[0] = (__bf16)lo;
+  v[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // Bit-exact IEEE half -> float (every binary16 value is exact in binary32),
@@ -115,6 +123,11 @@ enum SrcMode : int {
   SRC_Q8_R = 5,    // repacked Q8_0 planes, flat element e = k*ld + r
   SRC_Q4K_K = 6,   // repacked Q4_K planes, e = r*ld + k
   SRC_Q4K_R = 7,   // repacked Q4_K planes, e = k*ld + r
+  // "column planes": the same quantised values stored transposed so that the k index
+  // of a dX = dY W product is contiguous (bf16 GEMM only).
+  SRC_Q8T = 8,     // int8 p[r*ld + k], fp32 scale s[(r/32)*ld + k]
+  SRC_Q4KT = 9,    // 4-bit codes p[(r*ld + k)/2] (even k in the low nibble),
+                   // (sc*d, mn*dmin) float pairs s[2*((r/32)*ld + k) + {0,1}]
 };
 
 struct Operand {

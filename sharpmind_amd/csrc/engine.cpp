@@ -42,6 +42,8 @@ struct LayerW {
   DenseRef w[4], b[4];       // full-param weights [Out][In] and biases
   QuantPlanes q[4];          // LoRA mode frozen base
   void* qraw[4] = {};        // LoRA mode: planes storage
+  QuantPlanes qt[4];         // LoRA bf16 mode: column planes (transposed copy) for dX
+  void* qtraw[4] = {};
   DenseRef la[4], lb[4];     // LoRA A [In, nr], B [nr, Out]
   int* lb_cols = nullptr;    // device: column start of each diagonal block
 };
@@ -66,7 +68,7 @@ struct Engine {
   std::vector<void*> allocs;
   // tensors
   DenseRef emb, norm_f;
-  QuantPlanes emb_q{};
+  QuantPlanes emb_q{}, emb_qt{};
   std::vector<LayerW> L;
   std::map<std::string, DenseRef*> dense_by_name;
   // activations
@@ -190,6 +192,13 @@ static int build(Engine* e) {
     for (int l = 0; l < c.n_layers; l++)
       for (int p = 0; p < 4; p++)
         if (int rc = mk(&e->L[l].q[p], &e->L[l].qraw[p], (int64_t)e->Out[p] * e->In[p])) return rc;
+    if (e->bf) {  // column planes for the bf16 dX GEMMs
+      void* emb_t = nullptr;
+      if (int rc = mk(&e->emb_qt, &emb_t, (int64_t)V * d)) return rc;
+      for (int l = 0; l < c.n_layers; l++)
+        for (int p = 0; p < 4; p++)
+          if (int rc = mk(&e->L[l].qt[p], &e->L[l].qtraw[p], (int64_t)e->Out[p] * e->In[p])) return rc;
+    }
     for (int l = 0; l < c.n_layers; l++) {
       // column start of each diagonal block of the fused B: q|k|v at [0..3), gate|up at [3..5)
       LayerW& w = e->L[l];
@@ -297,6 +306,10 @@ static Operand w_fwd(const Engine* e, const LayerW& w, int p) {
 }
 // weight as the B operand of  dX = dY W  (n = In, k = Out)
 static Operand w_bwd(const Engine* e, const LayerW& w, int p) {
+  if (e->lora && e->bf) {
+    const QuantPlanes& q = w.qt[p];
+    return Operand{q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8T : SRC_Q4KT, q.qs, q.sc, e->Out[p]};
+  }
   if (e->lora) {
     const QuantPlanes& q = w.q[p];
     return Operand{q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8_R : SRC_Q4K_R, q.qs, q.sc, e->In[p]};
@@ -489,7 +502,8 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
     g.precision = prec(e); g.alpha = 1.f; g.split_k = 1;
     g.M = T; g.N = d; g.K = V;
     g.A = act_k(e, e->dlogits, V);
-    if (e->lora) g.B = Operand{e->emb_q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8_R : SRC_Q4K_R, e->emb_q.qs, e->emb_q.sc, d};
+    if (e->lora && e->bf) g.B = Operand{e->emb_qt.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8T : SRC_Q4KT, e->emb_qt.qs, e->emb_qt.sc, V};
+    else if (e->lora) g.B = Operand{e->emb_q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8_R : SRC_Q4K_R, e->emb_q.qs, e->emb_q.sc, d};
     else g.B = e->emb.bf ? Operand{SRC_BF16_R, e->emb.bf, nullptr, d} : Operand{SRC_F32_R, e->emb.data, nullptr, d};
     g.C = e->dx; g.ldc = d;
     g.split_k = split_for(T, d, V);
@@ -628,6 +642,17 @@ int smhip_engine_param_count(void* engine, int64_t* trainable, int64_t* frozen) 
   return SMHIP_OK;
 }
 
+// rebuild the column planes of row planes q (bf16 LoRA engines keep both)
+static int refresh_cols(Engine* e, const QuantPlanes* q, hipStream_t s) {
+  if (!e->bf || !e->lora) return SMHIP_OK;
+  QuantPlanes out;
+  if (q == &e->emb_q) return make_col_planes(*q, e->c.vocab, e->c.d_model, e->emb_qt.qs, &out, s);
+  for (auto& w : e->L)
+    for (int p = 0; p < 4; p++)
+      if (q == &w.q[p]) return make_col_planes(*q, e->Out[p], e->In[p], w.qt[p].qs, &out, s);
+  return fail(SMHIP_EINVAL, "engine: unknown quantised tensor");
+}
+
 static int parse_layer(const char* name, int* layer, std::string* rest) {
   if (name[0] != 'l' || !isdigit((unsigned char)name[1])) return 0;
   const char* dot = strchr(name, '.');
@@ -679,6 +704,7 @@ int smhip_engine_set_tensor(void* engine, const char* name, const void* host, in
       hipMemcpy(tmp, host, nbytes, hipMemcpyHostToDevice);
       QuantPlanes out;
       int rc = repack_planes(q->kind, tmp, q->n, q->qs, &out, nullptr);
+      if (!rc) rc = refresh_cols(e, q, nullptr);
       hipDeviceSynchronize();
       hipFree(tmp);
       return rc;
@@ -781,7 +807,8 @@ int smhip_engine_init_synthetic(void* engine, uint64_t seed) {
     if ((r2 = fill_normal(tmpf, q.n, next(), 0.f, 0.02f, s))) return r2;
     if ((r2 = encode_quant(q.kind, tmpf, q.n, tmpq, s))) return r2;
     QuantPlanes o;
-    return repack_planes(q.kind, tmpq, q.n, q.qs, &o, s);
+    if ((r2 = repack_planes(q.kind, tmpq, q.n, q.qs, &o, s))) return r2;
+    return refresh_cols(e, &q, s);
   };
   rc = quant(e->emb_q);
   for (int l = 0; l < c.n_layers && !rc; l++)

@@ -1,235 +1,259 @@
-// gemm_bf16.hip — high-throughput bf16 MFMA GEMM for gfx950 (the training step's linears).
+// gemm_bf16.hip — bf16 MFMA GEMM for gfx950 (every linear of the bf16 training step).
 //
 //   C[M,N] = alpha * sum_k A(m,k) B(n,k) [+ alpha2 * sum_k A2(m,k) B2(n,k)] [+ bias] [+ R] [+ beta C]
 //
-// Block tile BM x 128 x 64 (BM = 128 or 256), 256 threads = 4 wave64s in a 2 x 2
-// grid; each wave owns (BM/2) x 64 of C as 32 x 32 blocks of
-// v_mfma_f32_32x32x16_bf16.  Operands are staged into LDS as bf16 [row][64]
-// tiles (128-byte rows) whose 16-byte chunks are XOR-swizzled by row, so the
-// MFMA fragment reads (one ds_read_b128 per lane: 8 consecutive k of one row)
-// hit distinct banks.  Operand modes are template parameters:
-//   *_K  k-contiguous rows: 16-byte global loads straight into LDS chunks;
-//   *_R  row-contiguous (k-strided) matrices: each thread loads 4 k-rows x 8
-//        columns and writes 8 LDS quads (4 consecutive k of one row, 8 bytes),
-//        i.e. the transpose happens during staging;
-//   Q8 / Q4_K  frozen base weights: the repacked quantisation planes are
-//        decoded in registers (int8*scale, (sc*d)*v - mn*dmin; exact fp32 values
-//        rounded once to bf16) and never written to HBM dequantised.
-// The next K tile's global loads are issued before the current tile's MFMAs
-// (register prefetch + double-buffered LDS, one barrier per K tile).
-// Workgroups are numbered so that the 8 XCDs each own a contiguous band of
-// output tiles (AMD dispatches consecutive workgroups round-robin over XCDs),
-// keeping the operand panels a band shares in that XCD's L2.
+// Block tile BM x BN x 64 with 256 threads = 4 wave64s laid out WGM x WGN; each wave owns
+// a (BM/WGM) x (BN/WGN) block of C as 32 x 32 v_mfma_f32_32x32x16_bf16 tiles.  Operands
+// live in LDS as bf16 [row][64] tiles (128-byte rows) whose 16-byte chunks are XOR-swizzled
+// by row, so one ds_read_b128 per lane (8 consecutive k of one row: the MFMA fragment)
+// is bank-conflict free.  Operand staging by mode (template parameters):
+//   BF16_K   k-contiguous bf16: buffer_load ... lds (direct global -> LDS, no registers);
+//            each lane fetches the global chunk that belongs at its swizzled LDS slot;
+//   BF16_R   row-contiguous bf16: 4 k-rows x 8 columns per thread, transposed in
+//            registers, written as 8-byte LDS quads;
+//   Q8_K / Q4K_K   frozen base rows, Q8T / Q4KT   the same values as column planes
+//            (transposed copy for dX = dY W): int8 / 4-bit codes and their fp32 scales are
+//            loaded into registers and decoded (q*d, or (sc*d)*v - mn*dmin: the exact fp32
+//            weight) and rounded once to bf16 on the way into LDS.
+// All global loads are buffer loads whose resource covers exactly the operand: a row or
+// column beyond the matrix reads 0 (or, for row-contiguous operands, unrelated values that
+// only reach C rows/columns that are never stored), so the main loop has no guards.
+// Pipelining: the next K tile's loads (DMA or registers) are issued before the current
+// tile's MFMAs; double-buffered LDS, one barrier per K tile.
+// Workgroups are numbered so that each of the 8 XCDs owns a contiguous band of output
+// tiles (consecutive workgroups are dispatched round-robin over XCDs), swept in groups of 8
+// m-panels so that operand panels are reused from that XCD's L2.
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace smhip {
-namespace g2 {
+namespace g3 {
 
-constexpr int BN = 128, BK = 64, NT = 256;
+constexpr int BK = 64;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
+constexpr uint32_t OOB = 0x80000000u;  // any offset >= this reads 0 (resources are < 2 GiB)
 
 struct Op {
   const void* p;
   const float* s;
   int64_t ld;
+  int bytes;    // bytes of p covered by the buffer resource
+  int sbytes;   // bytes of s
 };
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // swizzled byte offset of 16-byte chunk c (0..7) of row r in a [rows][64] bf16 tile
 __device__ __forceinline__ int sw(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
-
 __device__ __forceinline__ uint32_t pk(float a, float b) { return pack_bf2(a, b); }
+// element of a vector register as float: copy to a scalar first (a bit cast applied directly
+// to a vector element reads element 0)
+__device__ __forceinline__ float as_f(uint32_t w) { return __builtin_bit_cast(float, w); }
 
-// ---------------------------------------------------------------- decode helpers (exact fp32, then bf16)
-__device__ __forceinline__ void i8x4(uint32_t w, float d, float* o) {
-  o[0] = (float)(int8_t)(w & 0xFF) * d;
-  o[1] = (float)(int8_t)((w >> 8) & 0xFF) * d;
-  o[2] = (float)(int8_t)((w >> 16) & 0xFF) * d;
-  o[3] = (float)(int8_t)(w >> 24) * d;
-}
-__device__ __forceinline__ void nib4(uint32_t w, int sh, float sd, float md, float* o) {
-  o[0] = sd * (float)((w >> sh) & 0xF) - md;
-  o[1] = sd * (float)((w >> (8 + sh)) & 0xF) - md;
-  o[2] = sd * (float)((w >> (16 + sh)) & 0xF) - md;
-  o[3] = sd * (float)((w >> (24 + sh)) & 0xF) - md;
-}
-
-// ---------------------------------------------------------------- K-contiguous operand (rows x 64)
-// Work is split into 16-byte global "units": bf16 unit = 8 elements, Q8 unit = 16 int8
-// elements; a tile row of 64 k is 8 (bf16) or 4 (Q8) units.
-template <int MODE, int ROWS>
-struct KLoader {
-  static constexpr bool BF = MODE == SRC_BF16_K;
-  static constexpr int EPU = BF ? 8 : 16;               // elements per unit
-  static constexpr int UPR = BK / EPU;                  // units per row
-  static constexpr int NU = ROWS * UPR / NT;            // units per thread
-  uint4 raw[NU];
-  float sc[NU];
-  __device__ __forceinline__ void load(const Op& o, int r0, int k0, int R) {
+// ---------------------------------------------------------------- BF16_K: direct to LDS
+// One wave instruction moves 64 x 16 B = 8 tile rows; lane l lands at LDS byte 16*l of the
+// instruction's 1 KiB block, i.e. row (l>>3), slot (l&7); it loads the global chunk whose
+// swizzled position is that slot.
+template <int ROWS, int NT>
+struct DmaLoad {
+  static constexpr int NW = NT / 64;
+  static_assert((ROWS / 8) % NW == 0, "tile rows must split evenly over the waves");
+  static constexpr int NI = ROWS / 8 / NW;  // instructions per wave per tile
+  uint32_t off[NI];
+  __amdgpu_buffer_rsrc_t rs;
+  __device__ __forceinline__ void init(const Op& o, int r0, int R) {
+    rs = rsrc(o.p, o.bytes);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
 #pragma unroll
-    for (int u = 0; u < NU; u++) {
-      const int id = u * NT + threadIdx.x;
-      const int r = id / UPR, c = id % UPR;
-      const int gr = r0 + r;
-      if (gr < R) {
-        const int64_t e = (int64_t)gr * o.ld + k0 + c * EPU;
-        if constexpr (BF) {
-          raw[u] = *reinterpret_cast<const uint4*>((const uint16_t*)o.p + e);
-        } else {
-          static_assert(MODE == SRC_Q8_K, "KLoader handles bf16 and Q8_0 rows");
-          raw[u] = *reinterpret_cast<const uint4*>((const int8_t*)o.p + e);
-          sc[u] = o.s[e >> 5];
-        }
-      } else {
-        raw[u] = make_uint4(0, 0, 0, 0);
-        sc[u] = 0.f;
-      }
+    for (int j = 0; j < NI; j++) {
+      const int r = (j * NW + w) * 8 + (l >> 3);
+      const int c = (l & 7) ^ ((r >> 1) & 7);
+      off[j] = (r0 + r < R) ? (uint32_t)(((int64_t)(r0 + r) * o.ld) * 2 + c * 16) : OOB;
     }
   }
-  __device__ __forceinline__ void store(uint8_t* lds) const {
+  __device__ __forceinline__ void fetch(uint8_t* tile, int k0) {
+    const int w = threadIdx.x >> 6;
+#if defined(__HIP_DEVICE_COMPILE__)  // the LDS address-space cast exists only in the device pass
 #pragma unroll
-    for (int u = 0; u < NU; u++) {
-      const int id = u * NT + threadIdx.x;
-      const int r = id / UPR, c = id % UPR;
-      if constexpr (BF) {
-        *reinterpret_cast<uint4*>(lds + sw(r, c)) = raw[u];
-      } else {
-        float v[16];
-        i8x4(raw[u].x, sc[u], v); i8x4(raw[u].y, sc[u], v + 4); i8x4(raw[u].z, sc[u], v + 8); i8x4(raw[u].w, sc[u], v + 12);
-        uint4 a, b;
-        a.x = pk(v[0], v[1]); a.y = pk(v[2], v[3]); a.z = pk(v[4], v[5]); a.w = pk(v[6], v[7]);
-        b.x = pk(v[8], v[9]); b.y = pk(v[10], v[11]); b.z = pk(v[12], v[13]); b.w = pk(v[14], v[15]);
-        *reinterpret_cast<uint4*>(lds + sw(r, 2 * c)) = a;
-        *reinterpret_cast<uint4*>(lds + sw(r, 2 * c + 1)) = b;
-      }
-    }
+    for (int j = 0; j < NI; j++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(tile + (j * NW + w) * 1024), 16, off[j] + k0 * 2, 0, 0, 0);
+#endif
   }
+  __device__ __forceinline__ void commit(uint8_t*) {}
 };
 
-// Q4_K K-contiguous needs 16 bytes of codes AND the shift: dedicated loader
-template <int ROWS>
-struct KLoaderQ4 {
-  static constexpr int UPR = BK / 16, NU = ROWS * UPR / NT;
-  uint4 raw[NU];
-  float sc[NU], sm[NU];
-  int sh[NU];
-  __device__ __forceinline__ void load(const Op& o, int r0, int k0, int R) {
-#pragma unroll
-    for (int u = 0; u < NU; u++) {
-      const int id = u * NT + threadIdx.x;
-      const int r = id / UPR, c = id % UPR;
-      const int gr = r0 + r;
-      if (gr < R) {
-        const int64_t e = (int64_t)gr * o.ld + k0 + c * 16;
-        const int w = (int)(e & 255);
-        raw[u] = *reinterpret_cast<const uint4*>((const uint8_t*)o.p + (e >> 8) * 128 + (w >> 6) * 32 + (w & 31));
-        sh[u] = ((w & 63) >> 5) * 4;
-        sc[u] = o.s[2 * (e >> 5)];
-        sm[u] = o.s[2 * (e >> 5) + 1];
-      } else {
-        raw[u] = make_uint4(0, 0, 0, 0);
-        sh[u] = 0; sc[u] = 0.f; sm[u] = 0.f;
-      }
-    }
-  }
-  __device__ __forceinline__ void store(uint8_t* lds) const {
-#pragma unroll
-    for (int u = 0; u < NU; u++) {
-      const int id = u * NT + threadIdx.x;
-      const int r = id / UPR, c = id % UPR;
-      float v[16];
-      nib4(raw[u].x, sh[u], sc[u], sm[u], v); nib4(raw[u].y, sh[u], sc[u], sm[u], v + 4);
-      nib4(raw[u].z, sh[u], sc[u], sm[u], v + 8); nib4(raw[u].w, sh[u], sc[u], sm[u], v + 12);
-      uint4 a, b;
-      a.x = pk(v[0], v[1]); a.y = pk(v[2], v[3]); a.z = pk(v[4], v[5]); a.w = pk(v[6], v[7]);
-      b.x = pk(v[8], v[9]); b.y = pk(v[10], v[11]); b.z = pk(v[12], v[13]); b.w = pk(v[14], v[15]);
-      *reinterpret_cast<uint4*>(lds + sw(r, 2 * c)) = a;
-      *reinterpret_cast<uint4*>(lds + sw(r, 2 * c + 1)) = b;
-    }
-  }
-};
-
-// ---------------------------------------------------------------- row-contiguous operand (k-strided)
-// Tile element (r, k) lives at e = (k0+k)*ld + r0 + r.  Each thread owns a
-// "quad": 4 consecutive k x 8 consecutive r; ROWS*64/32/256 quads per thread.
-template <int MODE, int ROWS>
-struct RLoader {
-  static constexpr int RG = ROWS / 8;          // row groups of 8
-  static constexpr int NQ = RG * (BK / 4) / NT; // quads per thread
-  uint2 raw[NQ][4];                             // bf16: 4 rows of 8 bf16 = 16 B (uint4) -> use two uint2
-  uint2 hi[NQ][4];
-  float sc[NQ][4], sm[NQ][4];
-  int sh[NQ][4];
-  __device__ __forceinline__ void load(const Op& o, int r0, int k0, int R) {
+// ---------------------------------------------------------------- BF16_R: k-strided, transposed in registers
+// quad = 4 consecutive k x 8 consecutive rows; (ROWS/8)*16 quads per tile.
+template <int ROWS, int NT>
+struct RLoad {
+  static constexpr int RG = ROWS / 8;
+  static constexpr int NQ_ALL = RG * (BK / 4);
+  static constexpr int NQ = NQ_ALL >= NT ? NQ_ALL / NT : 1;
+  u32x4 v[NQ][4];
+  uint32_t off[NQ];
+  uint32_t ldb;  // bytes per k row
+  __amdgpu_buffer_rsrc_t rs;
+  __device__ __forceinline__ bool active(int q) const { return NQ_ALL >= NT || (int)threadIdx.x < NQ_ALL; }
+  __device__ __forceinline__ void init(const Op& o, int r0, int R) {
+    rs = rsrc(o.p, o.bytes);
+    ldb = (uint32_t)(o.ld * 2);
 #pragma unroll
     for (int q = 0; q < NQ; q++) {
       const int id = q * NT + threadIdx.x;
       const int rg = id % RG, kq = id / RG;
-      const int gr = r0 + rg * 8;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int64_t e = (int64_t)(k0 + kq * 4 + j) * o.ld + gr;
-        if (gr + 8 <= R) {
-          if constexpr (MODE == SRC_BF16_R) {
-            uint4 a = *reinterpret_cast<const uint4*>((const uint16_t*)o.p + e);
-            raw[q][j] = make_uint2(a.x, a.y);
-            hi[q][j] = make_uint2(a.z, a.w);
-          } else if constexpr (MODE == SRC_Q8_R) {
-            raw[q][j] = *reinterpret_cast<const uint2*>((const int8_t*)o.p + e);
-            sc[q][j] = o.s[e >> 5];
-          } else {  // Q4K_R
-            const int w = (int)(e & 255);
-            raw[q][j] = *reinterpret_cast<const uint2*>((const uint8_t*)o.p + (e >> 8) * 128 + (w >> 6) * 32 + (w & 31));
-            sh[q][j] = ((w & 63) >> 5) * 4;
-            sc[q][j] = o.s[2 * (e >> 5)];
-            sm[q][j] = o.s[2 * (e >> 5) + 1];
-          }
-        } else {
-          raw[q][j] = make_uint2(0, 0);
-          hi[q][j] = make_uint2(0, 0);
-          sc[q][j] = 0.f; sm[q][j] = 0.f; sh[q][j] = 0;
-        }
-      }
+      off[q] = (uint32_t)(((int64_t)(kq * 4) * o.ld + r0 + rg * 8) * 2);
     }
   }
-  // element i (0..7) of the 8 columns at k-row j, as bf16 bits
-  __device__ __forceinline__ uint32_t el(int q, int j, int i) const {
-    if constexpr (MODE == SRC_BF16_R) {
-      const uint32_t w = i < 4 ? (i < 2 ? raw[q][j].x : raw[q][j].y) : (i < 6 ? hi[q][j].x : hi[q][j].y);
-      return (i & 1) ? (w >> 16) : (w & 0xFFFF);
-    } else if constexpr (MODE == SRC_Q8_R) {
-      const uint32_t w = i < 4 ? raw[q][j].x : raw[q][j].y;
-      return f2bf((float)(int8_t)((w >> (8 * (i & 3))) & 0xFF) * sc[q][j]);
-    } else {
-      const uint32_t w = i < 4 ? raw[q][j].x : raw[q][j].y;
-      return f2bf(sc[q][j] * (float)((w >> (8 * (i & 3) + sh[q][j])) & 0xF) - sm[q][j]);
-    }
-  }
-  __device__ __forceinline__ void store(uint8_t* lds) const {
+  __device__ __forceinline__ void fetch(uint8_t*, int k0) {
+    const uint32_t kb = (uint32_t)k0 * ldb;
 #pragma unroll
     for (int q = 0; q < NQ; q++) {
+      if (!active(q)) continue;
+#pragma unroll
+      for (int j = 0; j < 4; j++) v[q][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, off[q] + kb + j * ldb, 0, 0);
+    }
+  }
+  __device__ __forceinline__ void commit(uint8_t* tile) {
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+      if (!active(q)) continue;
       const int id = q * NT + threadIdx.x;
       const int rg = id % RG, kq = id / RG;
 #pragma unroll
       for (int i = 0; i < 8; i++) {
-        const int r = rg * 8 + i;
-        uint2 v;
-        v.x = el(q, 0, i) | (el(q, 1, i) << 16);
-        v.y = el(q, 2, i) | (el(q, 3, i) << 16);
-        // 4 consecutive k (8 bytes) = half of chunk kq/2
-        *reinterpret_cast<uint2*>(lds + sw(r, kq >> 1) + (kq & 1) * 8) = v;
+        const int w = i >> 1, hi = i & 1;
+        auto el = [&](int j) -> uint32_t { return hi ? (v[q][j][w] >> 16) : (v[q][j][w] & 0xFFFFu); };
+        u32x2 d;
+        d[0] = el(0) | (el(1) << 16);
+        d[1] = el(2) | (el(3) << 16);
+        *reinterpret_cast<u32x2*>(tile + sw(rg * 8 + i, kq >> 1) + (kq & 1) * 8) = d;
       }
     }
   }
 };
 
-template <int MODE, int ROWS>
-struct LoaderFor {
-  using T = typename std::conditional<(MODE & 1) == 0,
-                                      typename std::conditional<MODE == SRC_Q4K_K, KLoaderQ4<ROWS>, KLoader<MODE, ROWS>>::type,
-                                      RLoader<MODE, ROWS>>::type;
+// ---------------------------------------------------------------- quantised, k-contiguous in registers
+// unit = 16 consecutive k of one row (one 16-byte int8 load, or 8 bytes of 4-bit codes)
+template <int MODE, int ROWS, int NT>
+struct QLoad {
+  static constexpr int NU = ROWS * 4 / NT;
+  static_assert(NU >= 1, "quantised operand tile needs >= 64 rows");
+  static constexpr bool Q8 = MODE == SRC_Q8_K || MODE == SRC_Q8T;
+  static constexpr bool COL = MODE == SRC_Q8T || MODE == SRC_Q4KT;
+  // per-unit raw data
+  u32x4 q[NU];                 // Q8: 16 int8;  Q4K rows: 16 code bytes;  Q4KT: 8 code bytes in q.xy
+  float s[NU][COL ? 16 : 1];   // Q8 scales (one per unit for row planes, one per k for column planes)
+  float m[NU][Q8 ? 1 : (COL ? 16 : 1)];
+  uint32_t qoff[NU], soff[NU];
+  int shift[NU];
+  __amdgpu_buffer_rsrc_t rq, rsc;
+  __device__ __forceinline__ void init(const Op& o, int r0, int R) {
+    rq = rsrc(o.p, o.bytes);
+    rsc = rsrc(o.s, o.sbytes);
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+      const int id = u * NT + threadIdx.x;
+      const int r = id >> 2, kc = id & 3, row = r0 + r;
+      shift[u] = 0;
+      if (row >= R) { qoff[u] = OOB; soff[u] = OOB; continue; }
+      const int64_t e = (int64_t)row * o.ld + kc * 16;  // flat element index at k0 = 0
+      if constexpr (MODE == SRC_Q8_K) {
+        qoff[u] = (uint32_t)e;
+        soff[u] = (uint32_t)((e >> 5) * 4);
+      } else if constexpr (MODE == SRC_Q8T) {
+        qoff[u] = (uint32_t)e;
+        soff[u] = (uint32_t)(((int64_t)(row >> 5) * o.ld + kc * 16) * 4);
+      } else if constexpr (MODE == SRC_Q4K_K) {
+        // k0 is a multiple of 64 and ld of 256, so the in-super-block position of the unit
+        // shifts by k0 within a super-block: handled in fetch from the flat index
+        qoff[u] = (uint32_t)e;  // flat element index (decoded to a byte offset in fetch)
+        soff[u] = (uint32_t)((e >> 5) * 8);
+      } else {  // Q4KT
+        qoff[u] = (uint32_t)(e >> 1);
+        soff[u] = (uint32_t)(((int64_t)(row >> 5) * o.ld + kc * 16) * 8);
+      }
+    }
+  }
+  __device__ __forceinline__ void fetch(uint8_t*, int k0) {
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+      if constexpr (MODE == SRC_Q8_K) {
+        q[u] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff[u] + k0, 0, 0);
+        s[u][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, soff[u] + k0 / 8, 0, 0));
+      } else if constexpr (MODE == SRC_Q8T) {
+        q[u] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff[u] + k0, 0, 0);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rsc, soff[u] + k0 * 4 + c * 16, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; i++) s[u][c * 4 + i] = as_f(t[i]);
+        }
+      } else if constexpr (MODE == SRC_Q4K_K) {
+        const uint32_t e = qoff[u] == OOB ? OOB : qoff[u] + k0;
+        const uint32_t w = e & 255;
+        const uint32_t boff = e == OOB ? OOB : (e >> 8) * 128 + (w >> 6) * 32 + (w & 31);
+        shift[u] = ((w & 63) >> 5) * 4;
+        q[u] = __builtin_amdgcn_raw_buffer_load_b128(rq, boff, 0, 0);
+        const u32x2 p = __builtin_amdgcn_raw_buffer_load_b64(rsc, soff[u] + k0 / 4, 0, 0);
+        s[u][0] = as_f(p[0]);
+        m[u][0] = as_f(p[1]);
+      } else {  // Q4KT
+        const u32x2 c2 = __builtin_amdgcn_raw_buffer_load_b64(rq, qoff[u] + k0 / 2, 0, 0);
+        q[u][0] = c2[0];
+        q[u][1] = c2[1];
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+          const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rsc, soff[u] + k0 * 8 + c * 16, 0, 0);
+          s[u][2 * c] = as_f(t[0]);
+          m[u][2 * c] = as_f(t[1]);
+          s[u][2 * c + 1] = as_f(t[2]);
+          m[u][2 * c + 1] = as_f(t[3]);
+        }
+      }
+    }
+  }
+  __device__ __forceinline__ float val(int u, int i) const {
+    if constexpr (MODE == SRC_Q8_K) {
+      return (float)(int8_t)((q[u][i >> 2] >> (8 * (i & 3))) & 0xFF) * s[u][0];
+    } else if constexpr (MODE == SRC_Q8T) {
+      return (float)(int8_t)((q[u][i >> 2] >> (8 * (i & 3))) & 0xFF) * s[u][i];
+    } else if constexpr (MODE == SRC_Q4K_K) {
+      return s[u][0] * (float)((q[u][i >> 2] >> (8 * (i & 3) + shift[u])) & 0xF) - m[u][0];
+    } else {
+      return s[u][i] * (float)((q[u][i >> 3] >> (4 * (i & 7))) & 0xF) - m[u][i];
+    }
+  }
+  __device__ __forceinline__ void commit(uint8_t* tile) {
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+      const int id = u * NT + threadIdx.x;
+      const int r = id >> 2, kc = id & 3;
+      u32x4 a, b;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        a[i] = pk(val(u, 2 * i), val(u, 2 * i + 1));
+        b[i] = pk(val(u, 8 + 2 * i), val(u, 9 + 2 * i));
+      }
+      *reinterpret_cast<u32x4*>(tile + sw(r, 2 * kc)) = a;
+      *reinterpret_cast<u32x4*>(tile + sw(r, 2 * kc + 1)) = b;
+    }
+  }
 };
 
-// Rank-extension tile (LoRA): generic guarded element loads, any mode, K2 <= 64 per tile.
+template <int MODE, int ROWS, int NT>
+struct LoaderFor {
+  using T = typename std::conditional<
+      MODE == SRC_BF16_K, DmaLoad<ROWS, NT>,
+      typename std::conditional<MODE == SRC_BF16_R, RLoad<ROWS, NT>, QLoad<MODE, ROWS, NT>>::type>::type;
+};
+
+// ---------------------------------------------------------------- rank-extension tile (LoRA)
+// generic guarded element loads (bf16/fp32, k- or row-contiguous), K2 <= 256
 __device__ __forceinline__ float gen_elem(int mode, const Op& o, int r, int k, int R, int K) {
   if (r >= R || k >= K) return 0.f;
   switch (mode) {
@@ -239,17 +263,17 @@ __device__ __forceinline__ float gen_elem(int mode, const Op& o, int r, int k, i
     default: return ((const float*)o.p)[(int64_t)k * o.ld + r];
   }
 }
-template <int ROWS>
+template <int ROWS, int NT>
 __device__ __forceinline__ void gen_tile(int mode, const Op& o, int r0, int k0, int R, int K, float mult, uint8_t* lds) {
-  // thread handles 8 consecutive k of rows (ROWS*8 chunks)
   for (int c = threadIdx.x; c < ROWS * 8; c += NT) {
     const int r = c >> 3, ch = c & 7;
     float v[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) v[i] = mult * gen_elem(mode, o, r0 + r, k0 + ch * 8 + i, R, K);
-    uint4 a;
-    a.x = pk(v[0], v[1]); a.y = pk(v[2], v[3]); a.z = pk(v[4], v[5]); a.w = pk(v[6], v[7]);
-    *reinterpret_cast<uint4*>(lds + sw(r, ch)) = a;
+    u32x4 a;
+#pragma unroll
+    for (int i = 0; i < 4; i++) a[i] = pk(v[2 * i], v[2 * i + 1]);
+    *reinterpret_cast<u32x4*>(lds + sw(r, ch)) = a;
   }
 }
 
@@ -268,20 +292,29 @@ struct Args {
   float* partial;   // non-null: write raw partial sums [split][M][N] instead of C
 };
 
-template <int BM, int AMODE, int BMODE, bool C_BF16>
-__global__ __launch_bounds__(NT, BM == 128 ? 2 : 1) void gemm_bf16_kernel(Args g) {
-  constexpr int WM = BM / 2;       // rows per wave
-  constexpr int MB = WM / 32;      // 32-row blocks per wave
-  __shared__ __attribute__((aligned(16))) uint8_t sA[2][BM * 128];
-  __shared__ __attribute__((aligned(16))) uint8_t sB[2][BN * 128];
+template <int BM, int BN, int WGM, int NW>
+struct Shape {
+  static constexpr int NT = 64 * NW;
+  static constexpr int WGN = NW / WGM;
+  static constexpr int WM = BM / WGM, WN = BN / WGN;
+  static constexpr int MB = WM / 32, NB = WN / 32;
+  static constexpr int LDS = 2 * (BM + BN) * 128;
+  static constexpr int OCC = LDS * 2 <= 160 * 1024 && MB * NB <= 8 && NW == 4 ? 2 : 1;
+};
 
-  // XCD-aware tile order: workgroup w runs on XCD w % 8; give XCD x the contiguous band
-  // of tiles [x*per, (x+1)*per) (tile index = n-major within an m panel group).
+template <int BM, int BN, int WGM, int NW, int AMODE, int BMODE, bool C_BF16>
+__global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW>::OCC)) void gemm_kernel(Args g) {
+  using S = Shape<BM, BN, WGM, NW>;
+  constexpr int NT = S::NT;
+  constexpr int MB = S::MB, NB = S::NB;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[S::LDS];
+  auto sA = [&](int buf) -> uint8_t* { return smem + buf * (BM * 128); };
+  auto sB = [&](int buf) -> uint8_t* { return smem + 2 * BM * 128 + buf * (BN * 128); };
+
   const int ntiles = g.tiles_m * g.tiles_n;
   const int wg = blockIdx.x;
   int tile = wg;
   if (ntiles % 8 == 0) tile = (wg % 8) * (ntiles / 8) + wg / 8;
-  // within the band: groups of 8 m-panels swept along n (operand reuse in L2)
   constexpr int GM = 8;
   const int group = tile / (GM * g.tiles_n);
   const int first_m = group * GM;
@@ -291,75 +324,79 @@ __global__ __launch_bounds__(NT, BM == 128 ? 2 : 1) void gemm_bf16_kernel(Args g
   const int m0 = tm * BM, n0 = tn * BN;
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int wm = wv >> 1, wn = wv & 1;
+  const int wm = wv / S::WGN, wn = wv % S::WGN;
 
-  floatx16 acc[MB][2];
+  floatx16 acc[MB][NB];
 #pragma unroll
   for (int i = 0; i < MB; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < NB; j++)
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
-  typename LoaderFor<AMODE, BM>::T la;
-  typename LoaderFor<BMODE, BN>::T lb;
+  typename LoaderFor<AMODE, BM, NT>::T la;
+  typename LoaderFor<BMODE, BN, NT>::T lb;
+  la.init(g.A, m0, g.M);
+  lb.init(g.B, n0, g.N);
+
   const int nk_all = g.K / BK;
   const int split = blockIdx.y, nsplit = gridDim.y;
   const int kt0 = split * g.kps;
-  const int nk1 = max(0, min(nk_all, kt0 + g.kps) - kt0);           // main K tiles of this split
-  const int nk2 = split == nsplit - 1 ? (g.K2 + BK - 1) / BK : 0;   // rank extension: last split only
-  const int nt = nk1 + nk2;
+  const int nk1 = max(0, min(nk_all, kt0 + g.kps) - kt0);
+  const int nk2 = split == nsplit - 1 ? (g.K2 + BK - 1) / BK : 0;
 
+  // fragments of k-slice kk+1 are read from LDS while the MFMAs of slice kk run
   auto compute = [&](int buf) {
-    const uint8_t* a = sA[buf];
-    const uint8_t* b = sB[buf];
+    const uint8_t* a = sA(buf);
+    const uint8_t* b = sB(buf);
+    bf16x8 fa[2][MB], fb[2][NB];
+    auto rd = [&](int kk, int p) {
+      const int ch = 2 * kk + (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < MB; i++) fa[p][i] = *reinterpret_cast<const bf16x8*>(a + sw(wm * S::WM + i * 32 + (lane & 31), ch));
+#pragma unroll
+      for (int j = 0; j < NB; j++) fb[p][j] = *reinterpret_cast<const bf16x8*>(b + sw(wn * S::WN + j * 32 + (lane & 31), ch));
+    };
+    rd(0, 0);
 #pragma unroll
     for (int kk = 0; kk < BK / 16; kk++) {
-      const int ch = 2 * kk + (lane >> 5);
-      bf16x8 fa[MB], fb[2];
-#pragma unroll
-      for (int i = 0; i < MB; i++) {
-        const int r = wm * WM + i * 32 + (lane & 31);
-        fa[i] = *reinterpret_cast<const bf16x8*>(a + sw(r, ch));
-      }
-#pragma unroll
-      for (int j = 0; j < 2; j++) {
-        const int r = wn * 64 + j * 32 + (lane & 31);
-        fb[j] = *reinterpret_cast<const bf16x8*>(b + sw(r, ch));
-      }
+      if (kk + 1 < BK / 16) rd(kk + 1, (kk + 1) & 1);
+      const int p = kk & 1;
 #pragma unroll
       for (int i = 0; i < MB; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < NB; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[p][i], fb[p][j], acc[i][j], 0, 0, 0);
     }
   };
 
   if (nk1 > 0) {
-    la.load(g.A, m0, kt0 * BK, g.M);
-    lb.load(g.B, n0, kt0 * BK, g.N);
-    la.store(sA[0]);
-    lb.store(sB[0]);
-  } else if (nk2 > 0) {
-    gen_tile<BM>(g.amode2, g.A2, m0, 0, g.M, g.K2, g.alpha2, sA[0]);
-    gen_tile<BN>(g.bmode2, g.B2, n0, 0, g.N, g.K2, 1.f, sB[0]);
+    la.fetch(sA(0), kt0 * BK);
+    lb.fetch(sB(0), kt0 * BK);
+    la.commit(sA(0));
+    lb.commit(sB(0));
+    wait_vm();
+    __syncthreads();
+    for (int t = 0; t < nk1; t++) {
+      const int buf = t & 1;
+      const bool more = t + 1 < nk1;
+      if (more) {
+        la.fetch(sA(buf ^ 1), (kt0 + t + 1) * BK);
+        lb.fetch(sB(buf ^ 1), (kt0 + t + 1) * BK);
+      }
+      compute(buf);
+      if (more) {
+        la.commit(sA(buf ^ 1));
+        lb.commit(sB(buf ^ 1));
+      }
+      wait_vm();
+      __syncthreads();
+    }
   }
-  __syncthreads();
-  for (int t = 0; t < nt; t++) {
-    const int buf = t & 1;
-    const bool next_main = t + 1 < nk1;
-    if (next_main) {
-      la.load(g.A, m0, (kt0 + t + 1) * BK, g.M);
-      lb.load(g.B, n0, (kt0 + t + 1) * BK, g.N);
-    }
-    compute(buf);
-    if (next_main) {
-      la.store(sA[buf ^ 1]);
-      lb.store(sB[buf ^ 1]);
-    } else if (t + 1 < nt) {
-      const int k0 = (t + 1 - nk1) * BK;
-      gen_tile<BM>(g.amode2, g.A2, m0, k0, g.M, g.K2, g.alpha2, sA[buf ^ 1]);
-      gen_tile<BN>(g.bmode2, g.B2, n0, k0, g.N, g.K2, 1.f, sB[buf ^ 1]);
-    }
+  for (int t = 0; t < nk2; t++) {  // rank extension (all waves are past the last main-tile barrier)
+    gen_tile<BM, NT>(g.amode2, g.A2, m0, t * BK, g.M, g.K2, g.alpha2, sA(0));
+    gen_tile<BN, NT>(g.bmode2, g.B2, n0, t * BK, g.N, g.K2, 1.f, sB(0));
+    __syncthreads();
+    compute(0);
     __syncthreads();
   }
 
@@ -367,13 +404,13 @@ __global__ __launch_bounds__(NT, BM == 128 ? 2 : 1) void gemm_bf16_kernel(Args g
 #pragma unroll
   for (int i = 0; i < MB; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+    for (int j = 0; j < NB; j++) {
+      const int col = n0 + wn * S::WN + j * 32 + (lane & 31);
       if (col >= g.N) continue;
       const float bv = g.bias ? g.bias[col] : 0.f;
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        const int row = m0 + wm * WM + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        const int row = m0 + wm * S::WM + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
         if (row >= g.M) continue;
         if (g.partial) {
           g.partial[((int64_t)split * g.M + row) * g.N + col] = acc[i][j][e];
@@ -392,33 +429,6 @@ __global__ __launch_bounds__(NT, BM == 128 ? 2 : 1) void gemm_bf16_kernel(Args g
         }
       }
     }
-}
-
-template <int BM, int AM, int BMD>
-static void launch_c(const Args& a, int c_bf16, int splits, hipStream_t s) {
-  const dim3 grid(a.tiles_m * a.tiles_n, splits);
-  if (c_bf16 && !a.partial) hipLaunchKernelGGL((gemm_bf16_kernel<BM, AM, BMD, true>), grid, dim3(NT), 0, s, a);
-  else hipLaunchKernelGGL((gemm_bf16_kernel<BM, AM, BMD, false>), grid, dim3(NT), 0, s, a);
-}
-
-template <int BM>
-static bool dispatch(const Args& a, int amode, int bmode, int c_bf16, int sp, hipStream_t s) {
-  if (amode == SRC_BF16_K) {
-    switch (bmode) {
-      case SRC_BF16_K: launch_c<BM, SRC_BF16_K, SRC_BF16_K>(a, c_bf16, sp, s); return true;
-      case SRC_BF16_R: launch_c<BM, SRC_BF16_K, SRC_BF16_R>(a, c_bf16, sp, s); return true;
-      case SRC_Q8_K: launch_c<BM, SRC_BF16_K, SRC_Q8_K>(a, c_bf16, sp, s); return true;
-      case SRC_Q8_R: launch_c<BM, SRC_BF16_K, SRC_Q8_R>(a, c_bf16, sp, s); return true;
-      case SRC_Q4K_K: launch_c<BM, SRC_BF16_K, SRC_Q4K_K>(a, c_bf16, sp, s); return true;
-      case SRC_Q4K_R: launch_c<BM, SRC_BF16_K, SRC_Q4K_R>(a, c_bf16, sp, s); return true;
-      default: return false;
-    }
-  }
-  if (amode == SRC_BF16_R && bmode == SRC_BF16_R && (!c_bf16 || a.partial)) {
-    launch_c<BM, SRC_BF16_R, SRC_BF16_R>(a, 0, sp, s);
-    return true;
-  }
-  return false;
 }
 
 // C = alpha * sum_s partial[s] (+ bias) (+ R) (+ beta C); splits summed in ascending order.
@@ -445,35 +455,128 @@ __global__ void splitk_epilogue_kernel(const float* __restrict__ partial, int sp
   }
 }
 
-}  // namespace g2
+// ---------------------------------------------------------------- host dispatch
+// 256x256 runs 8 waves (2 x 4, each 128 x 64); the others 4 waves.
+enum TileId { T256x256 = 0, T256x128 = 1, T128x128 = 2, T256x64 = 3, NTILE = 4 };
+struct TileInfo { int bm, bn, occ; double eff; };
+// eff: relative MFMA throughput per CU of the tile shape (larger tiles re-read less LDS/L2)
+static const TileInfo kTiles[NTILE] = {
+    {256, 256, Shape<256, 256, 2, 8>::OCC, 1.00},  // measured 4096^3 bf16: 972 TF/s
+    {256, 128, Shape<256, 128, 2, 4>::OCC, 0.69},  //                         673
+    {128, 128, Shape<128, 128, 2, 4>::OCC, 0.88},  //                         856
+    {256, 64, Shape<256, 64, 4, 4>::OCC, 0.60},
+};
+
+template <int BM, int BN, int WGM, int NW, int AM, int BMD>
+static void launch_c(const Args& a, int c_bf16, int splits, hipStream_t s) {
+  const dim3 grid(a.tiles_m * a.tiles_n, splits);
+  if (c_bf16 && !a.partial) hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, true>), grid, dim3(64 * NW), 0, s, a);
+  else hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, false>), grid, dim3(64 * NW), 0, s, a);
+}
+
+template <int AM, int BMD>
+static void launch_tile(int tile, const Args& a, int c_bf16, int sp, hipStream_t s) {
+  switch (tile) {
+    case T256x256: launch_c<256, 256, 2, 8, AM, BMD>(a, c_bf16, sp, s); break;
+    case T256x128: launch_c<256, 128, 2, 4, AM, BMD>(a, c_bf16, sp, s); break;
+    case T128x128: launch_c<128, 128, 2, 4, AM, BMD>(a, c_bf16, sp, s); break;
+    default: launch_c<256, 64, 4, 4, AM, BMD>(a, c_bf16, sp, s); break;
+  }
+}
+
+static bool dispatch(int tile, const Args& a, int amode, int bmode, int c_bf16, int sp, hipStream_t s) {
+  if (amode == SRC_BF16_K) {
+    switch (bmode) {
+      case SRC_BF16_K: launch_tile<SRC_BF16_K, SRC_BF16_K>(tile, a, c_bf16, sp, s); return true;
+      case SRC_BF16_R: launch_tile<SRC_BF16_K, SRC_BF16_R>(tile, a, c_bf16, sp, s); return true;
+      case SRC_Q8_K: launch_tile<SRC_BF16_K, SRC_Q8_K>(tile, a, c_bf16, sp, s); return true;
+      case SRC_Q8T: launch_tile<SRC_BF16_K, SRC_Q8T>(tile, a, c_bf16, sp, s); return true;
+      case SRC_Q4K_K: launch_tile<SRC_BF16_K, SRC_Q4K_K>(tile, a, c_bf16, sp, s); return true;
+      case SRC_Q4KT: launch_tile<SRC_BF16_K, SRC_Q4KT>(tile, a, c_bf16, sp, s); return true;
+      default: return false;
+    }
+  }
+  if (amode == SRC_BF16_R && bmode == SRC_BF16_R && (!c_bf16 || a.partial)) {
+    launch_tile<SRC_BF16_R, SRC_BF16_R>(tile, a, 0, sp, s);
+    return true;
+  }
+  return false;
+}
+
+// pick the tile shape with the smallest estimated time: whole "rounds" of resident
+// workgroups times the per-tile work divided by the shape's efficiency
+static int pick_tile(int M, int N, int splits, int bmode) {
+  static const int forced = [] {  // SMHIP_GEMM_TILE=0..3 pins the tile shape (tuning runs)
+    const char* v = getenv("SMHIP_GEMM_TILE");
+    return v ? atoi(v) : -1;
+  }();
+  if (forced >= 0 && forced < NTILE && !(forced == T256x64 && N > 64)) return forced;
+  const int cus = num_cus();
+  int best = T128x128;
+  double best_t = 1e300;
+  for (int t = 0; t < NTILE; t++) {
+    const TileInfo& ti = kTiles[t];
+    if (t == T256x64 && N > 64) continue;
+    const int64_t tiles = (int64_t)ceil_div(M, ti.bm) * ceil_div(N, ti.bn) * splits;
+    const int64_t slots = (int64_t)cus * ti.occ;
+    const double rounds = (double)((tiles + slots - 1) / slots);
+    const double est = rounds * ti.occ * (double)ti.bm * ti.bn / ti.eff;
+    if (est < best_t * 0.999) { best_t = est; best = t; }
+  }
+  return best;
+}
+
+}  // namespace g3
 
 static bool aligned_16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// bytes spanned by an operand with rows x K elements (element width by mode)
+static int64_t op_bytes(const Operand& o, int rows, int K, int64_t* sbytes) {
+  *sbytes = 0;
+  switch (o.mode) {
+    case SRC_BF16_K: return ((int64_t)(rows - 1) * o.ld + K) * 2;
+    case SRC_BF16_R: return ((int64_t)(K - 1) * o.ld + rows) * 2;
+    case SRC_Q8_K: *sbytes = ((int64_t)(rows - 1) * o.ld + K) / 32 * 4; return (int64_t)(rows - 1) * o.ld + K;
+    case SRC_Q8T: *sbytes = ((int64_t)((rows - 1) / 32) * o.ld + K) * 4; return (int64_t)(rows - 1) * o.ld + K;
+    case SRC_Q4K_K: *sbytes = ((int64_t)(rows - 1) * o.ld + K) / 32 * 8; return ((int64_t)(rows - 1) * o.ld + K) / 2;
+    case SRC_Q4KT: *sbytes = ((int64_t)((rows - 1) / 32) * o.ld + K) * 8; return ((int64_t)(rows - 1) * o.ld + K) / 2;
+    default: return -1;
+  }
+}
+
 // Returns 1 if the fast path ran, 0 if the shape/modes need the generic kernel, <0 on error.
 int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
-  using namespace g2;
+  using namespace g3;
   if (g.precision != SMHIP_PREC_BF16) return 0;
   if (g.K % BK != 0 || g.K2 > 4 * BK) return 0;
   const int am = g.A.mode, bm = g.B.mode;
   const bool a_ok = am == SRC_BF16_K || am == SRC_BF16_R;
-  const bool b_ok = bm == SRC_BF16_K || bm == SRC_BF16_R || bm == SRC_Q8_K || bm == SRC_Q8_R || bm == SRC_Q4K_K || bm == SRC_Q4K_R;
+  const bool b_ok = bm == SRC_BF16_K || bm == SRC_BF16_R || bm == SRC_Q8_K || bm == SRC_Q8T || bm == SRC_Q4K_K || bm == SRC_Q4KT;
   if (!a_ok || !b_ok) return 0;
-  // alignment of every vector load: rows of 16 B (bf16 K: ld%8; quant: ld%32; R-modes: 8-column groups)
+  if (am == SRC_BF16_R && bm != SRC_BF16_R) return 0;
   if (!aligned_16(g.A.p) || !aligned_16(g.B.p)) return 0;
   if (am == SRC_BF16_K && g.A.ld % 8) return 0;
-  if (am == SRC_BF16_R && (g.A.ld % 8 || g.M % 8)) return 0;
-  if ((bm == SRC_BF16_K) && g.B.ld % 8) return 0;
-  if ((bm == SRC_BF16_R) && (g.B.ld % 8 || g.N % 8)) return 0;
-  if (bm >= SRC_Q8_K && (g.B.ld % 32 || g.N % 8)) return 0;
+  if (am == SRC_BF16_R && (g.A.ld % 8 || (uintptr_t)g.A.p % 16)) return 0;
+  if (bm == SRC_BF16_K && g.B.ld % 8) return 0;
+  if (bm == SRC_BF16_R && g.B.ld % 8) return 0;
+  if ((bm == SRC_Q8_K || bm == SRC_Q8T || bm == SRC_Q4KT) && g.B.ld % 32) return 0;
+  if (bm == SRC_Q4K_K && g.B.ld % 256) return 0;
+  if ((bm == SRC_Q8T || bm == SRC_Q4KT) && !aligned_16(g.B.s)) return 0;
   if (g.K2 > 0) {
     for (int m : {g.A2.mode, g.B2.mode})
       if (m != SRC_BF16_K && m != SRC_BF16_R && m != SRC_F32_K && m != SRC_F32_R) return 0;
   }
+  int64_t asb = 0, bsb = 0;
+  const int64_t ab = op_bytes(g.A, g.M, g.K, &asb), bb = op_bytes(g.B, g.N, g.K, &bsb);
+  // 32-bit buffer offsets: every operand (and any row beyond it) below 2 GiB
+  const int64_t lim = (int64_t)1 << 31;
+  if (ab < 0 || bb < 0 || ab + 256 * 4 * g.A.ld >= lim || bb + 256 * 4 * g.B.ld >= lim || bsb >= lim) return 0;
+
   Args a;
-  a.A = {g.A.p, g.A.s, g.A.ld};
-  a.B = {g.B.p, g.B.s, g.B.ld};
-  a.A2 = {g.A2.p, g.A2.s, g.A2.ld};
-  a.B2 = {g.B2.p, g.B2.s, g.B2.ld};
+  a.A = {g.A.p, g.A.s, g.A.ld, (int)ab, 0};
+  a.B = {g.B.p, g.B.s, g.B.ld, (int)bb, (int)bsb};
+  a.A2 = {g.A2.p, g.A2.s, g.A2.ld, 0, 0};
+  a.B2 = {g.B2.p, g.B2.s, g.B2.ld, 0, 0};
   a.amode2 = g.A2.mode;
   a.bmode2 = g.B2.mode;
   a.M = g.M; a.N = g.N; a.K = g.K; a.K2 = g.K2;
@@ -482,23 +585,20 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   a.beta = g.beta;
   a.C = g.C; a.ldc = g.ldc;
   a.bias = g.bias; a.R = g.R; a.ldr = g.ldr;
-  a.tiles_n = ceil_div(g.N, BN);
-  // 256-row tiles when they still give >= 2 workgroups per CU worth of tiles
-  const int t256 = ceil_div(g.M, 256) * a.tiles_n;
-  const bool big = t256 >= 2 * num_cus();
-  a.tiles_m = ceil_div(g.M, big ? 256 : 128);
   const int nk = g.K / BK;
   int sp = std::max(1, std::min(g.split_k, nk));
   a.kps = ceil_div(nk, sp);
   sp = ceil_div(nk, a.kps);
+  const int tile = pick_tile(g.M, g.N, sp, bm);
+  a.tiles_m = ceil_div(g.M, kTiles[tile].bm);
+  a.tiles_n = ceil_div(g.N, kTiles[tile].bn);
   a.partial = nullptr;
   if (sp > 1) {
     a.partial = (float*)workspace(s, sizeof(float) * (size_t)sp * g.M * g.N, 3);
     if (!a.partial) return fail(SMHIP_ENOMEM, "gemm: split-K workspace");
   }
   const int ev0 = prof_mark(s);
-  const bool ok = big ? dispatch<256>(a, am, bm, g.c_bf16, sp, s) : dispatch<128>(a, am, bm, g.c_bf16, sp, s);
-  if (!ok) return 0;
+  if (!dispatch(tile, a, am, bm, g.c_bf16, sp, s)) return 0;
   SMHIP_CHECK_LAUNCH();
   prof_add(PROF_GEMM, ev0, prof_mark(s), 2.0 * g.M * g.N * ((double)g.K + g.K2), g.M, g.N, g.K + g.K2);
   if (sp > 1) {

@@ -45,6 +45,7 @@ int dequant_raw(int qtype, const void* raw, float* out, int64_t n, hipStream_t s
 size_t planes_bytes(int qtype, int64_t n, size_t* qs_bytes);
 int repack_planes(int qtype, const void* raw, int64_t n, void* dst, QuantPlanes* out, hipStream_t s);
 int dequant_rows(const QuantPlanes& q, const int32_t* ids, float* out, int T, int D, hipStream_t s);
+int make_col_planes(const QuantPlanes& q, int rows, int cols, void* dst, QuantPlanes* out, hipStream_t s);
 
 // attention.hip
 int attention_slot_backward(const float* dO, const float* q, const float* k, const float* v,

@@ -135,6 +135,65 @@ int repack_planes(int qtype, const void* raw, int64_t n, void* dst, QuantPlanes*
   return SMHIP_OK;
 }
 
+// ---------------------------------------------------------------- column planes
+// The transposed copy of a [rows][cols] quantised matrix used by dX = dY W: element
+// (o, i) of the row planes becomes element i*rows + o, with the fp32 scale (Q8_0) or the
+// (sc*d, mn*dmin) pair (Q4_K) of its 32-block stored at (i/32)*rows + o, so that a run of
+// consecutive o (the k index of dX) is contiguous in both planes.  Same values, same bits.
+__global__ void col_planes_q8_kernel(const int8_t* __restrict__ qs, const float* __restrict__ sc, int rows, int cols,
+                                     int8_t* __restrict__ qt, float* __restrict__ st) {
+  const int64_t n = (int64_t)rows * cols;
+  const int cb = cols / 32;
+  for (int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; x < n; x += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = x / rows, o = x - i * rows;
+    qt[x] = qs[o * cols + i];
+    if ((i & 31) == 0) st[(i >> 5) * rows + o] = sc[o * cb + (i >> 5)];
+  }
+}
+__device__ __forceinline__ uint32_t q4k_code(const uint8_t* qs, int64_t e) {
+  const int w = (int)(e & 255);
+  return (qs[(e >> 8) * 128 + (w >> 6) * 32 + (w & 31)] >> (((w & 63) >> 5) * 4)) & 0xF;
+}
+__global__ void col_planes_q4k_kernel(const uint8_t* __restrict__ qs, const float* __restrict__ sm, int rows, int cols,
+                                      uint8_t* __restrict__ qt, float* __restrict__ st) {
+  const int64_t n2 = (int64_t)rows * cols / 2;  // one output byte = codes of (o, i) and (o+1, i), o even
+  const int cb = cols / 32;
+  for (int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; x < n2; x += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t f = 2 * x, i = f / rows, o = f - i * rows;
+    const uint32_t lo = q4k_code(qs, o * cols + i), hi = q4k_code(qs, (o + 1) * cols + i);
+    qt[x] = (uint8_t)(lo | (hi << 4));
+    if ((i & 31) == 0) {
+      for (int j = 0; j < 2; j++) {
+        const int64_t src = 2 * ((o + j) * cb + (i >> 5)), dst = 2 * ((i >> 5) * rows + o + j);
+        st[dst] = sm[src];
+        st[dst + 1] = sm[src + 1];
+      }
+    }
+  }
+}
+int make_col_planes(const QuantPlanes& q, int rows, int cols, void* dst, QuantPlanes* out, hipStream_t s) {
+  SMHIP_REQUIRE(q.n == (int64_t)rows * cols, "column planes: shape does not match the planes");
+  SMHIP_REQUIRE(cols % 32 == 0 && rows % 2 == 0, "column planes: cols must be a multiple of 32, rows even");
+  size_t qb = 0;
+  planes_bytes(q.kind, q.n, &qb);
+  out->kind = q.kind;
+  out->n = q.n;
+  out->qs = dst;
+  out->sc = (float*)((char*)dst + qb);
+  const int64_t n = q.kind == SMHIP_QTYPE_Q8_0 ? q.n : q.n / 2;
+  const int g = (int)std::min<int64_t>((n + 255) / 256, (int64_t)num_cus() * 16);
+  if (q.kind == SMHIP_QTYPE_Q8_0)
+    hipLaunchKernelGGL(col_planes_q8_kernel, dim3(g), dim3(256), 0, s, (const int8_t*)q.qs, q.sc, rows, cols,
+                       (int8_t*)out->qs, out->sc);
+  else if (q.kind == SMHIP_QTYPE_Q4_K)
+    hipLaunchKernelGGL(col_planes_q4k_kernel, dim3(g), dim3(256), 0, s, (const uint8_t*)q.qs, q.sc, rows, cols,
+                       (uint8_t*)out->qs, out->sc);
+  else
+    return fail(SMHIP_EUNSUPPORTED, "column planes: qtype must be Q8_0 (8) or Q4_K (12)");
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
 }  // namespace smhip
 
 namespace smhip {

@@ -91,7 +91,8 @@ def run_pair(orc, dev, c, seed=0, tol=1e-5, params=None, ids=None, loss_tol=None
     assert errs["loss"] <= (tol if loss_tol is None else loss_tol), errs["loss"]
     worst = max(errs.items(), key=lambda kv: kv[1])
     print(f"worst {worst}, loss gpu {got_loss} oracle {ref_loss}")
-    assert worst[1] <= tol, worst
+    bad = sorted(((k, v) for k, v in errs.items() if v > tol), key=lambda kv: -kv[1])
+    assert not bad, bad[:12]
     return eng, P, G, ids, labels
 
 

@@ -46,3 +46,34 @@ def test_gemm_modes(dev, M, N, K, am, bm, split, c_bf16):
         ref = 0.5 * (a.astype(np.float64) @ b.astype(np.float64).T) + beta * c0
         tol = 2e-2 if c_bf16 else 1e-5
         assert rel_err(tc.float().cpu().numpy(), ref) <= tol, (beta, rel_err(tc.float().cpu().numpy(), ref))
+
+
+@pytest.mark.parametrize("qtype", [8, 12])
+@pytest.mark.parametrize("trans", [0, 1])
+@pytest.mark.parametrize("M,N,K", [(300, 256, 512), (4096, 512, 256), (64, 1024, 768), (1000, 768, 256)])
+def test_qgemm_bf16(orc, dev, qtype, trans, M, N, K):
+    """Dequant-fused GEMM through Q8_0 / Q4_K weights, both directions (forward rows and
+    the dX column planes), against float64 on the bf16-rounded bit-exact dequantised weights."""
+    rng = np.random.default_rng(M + N + K + qtype + trans)
+    shape = (K, N) if trans else (N, K)
+    w = (rng.standard_normal(shape) * 0.05).astype(np.float32).ravel()
+    if qtype == 8:
+        raw = np.zeros(w.size // 32 * 34, np.uint8)
+        assert orc.orc_quantize_q8_0(w, w.size, raw) == 0
+        deq = np.zeros_like(w)
+        orc.orc_dequant_q8_0(raw, deq, w.size)
+    else:
+        raw = np.zeros(w.size // 256 * 144, np.uint8)
+        assert orc.orc_quantize_q4k(w, w.size, raw) == 0
+        deq = np.zeros_like(w)
+        orc.orc_dequant_q4k(raw, deq, w.size)
+    wb = torch.from_numpy(deq).to(torch.bfloat16).float().numpy().reshape(shape).astype(np.float64)
+    a = _rnd((M, K), rng)
+    ta = torch.from_numpy(a).to(dev).to(torch.bfloat16)
+    tc = torch.zeros(M, N, device=dev)
+    check(sharpmind_amd.lib().smhip_qgemm_bf16(qtype, trans, M, N, K, ta.data_ptr(), K,
+                                               torch.from_numpy(raw).to(dev).data_ptr(), tc.data_ptr(), N,
+                                               torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    ref = a.astype(np.float64) @ (wb if trans else wb.T)
+    assert rel_err(tc.cpu().numpy(), ref) <= 1e-5, rel_err(tc.cpu().numpy(), ref)
