@@ -19,7 +19,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("SMHIP_ARCH", "gfx950")
 
 CFLAGS = [
-    "-x", "hip", f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
+    "-x", "hip", f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++20",
     "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result", "-I", os.path.join(HERE, "..", "include"),
 ]

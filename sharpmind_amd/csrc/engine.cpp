@@ -319,13 +319,14 @@ static Operand w_bwd(const Engine* e, const LayerW& w, int p) {
 static int prec(const Engine* e) { return e->bf ? SMHIP_PREC_BF16 : SMHIP_PREC_FP32; }
 static float lora_scale(const Engine* e) { return e->c.lora_alpha / (float)e->c.lora_rank; }
 
-// split-K factor: enough workgroups (about 2 per CU) for GEMMs whose output has few 128x128 tiles
+// split-K factor: enough workgroups (2 per CU, the occupancy of the 128x128 tile) for GEMMs
+// whose output has few 128x128 tiles, keeping >= 8 K tiles of 64 per split
 static int split_for(int M, int N, int K) {
   const int tiles = ceil_div(M, 128) * ceil_div(N, 128);
   const int kt = K / 64;
-  if (tiles >= num_cus() || kt < 4) return 1;
-  int s = (2 * num_cus()) / tiles;
-  s = std::min(s, kt / 2);
+  if (tiles >= 2 * num_cus() || kt < 16) return 1;
+  int s = ceil_div(2 * num_cus(), tiles);
+  s = std::min(s, kt / 8);
   return std::max(1, std::min(s, 32));
 }
 
@@ -360,6 +361,7 @@ static int proj_forward(Engine* e, int l, int p, const void* x, void* y, int y_b
     g.alpha2 = lora_scale(e);
   }
   g.M = T; g.N = Out; g.K = In;
+  g.split_k = split_for(T, Out, In);
   g.A = act_k(e, x, In);
   g.B = w_fwd(e, w, p);
   g.C = y; g.ldc = Out; g.c_bf16 = y_bf16;
@@ -434,6 +436,7 @@ static int proj_backward(Engine* e, int l, int p, const void* dY, const float* d
     }
   }
   g.M = T; g.N = In; g.K = Out;
+  g.split_k = split_for(T, In, Out);
   g.A = act_k(e, dY, Out);
   g.B = w_bwd(e, w, p);
   g.C = dX_out ? dX_out : (void*)dX; g.ldc = In; g.c_bf16 = dX_bf16;
