@@ -330,6 +330,9 @@ static int split_for(int M, int N, int K) {
   return std::max(1, std::min(s, 32));
 }
 
+// bf16 engines let the GEMM choose the split (0 = automatic); fp32 (exactness) engines use split_for
+static int split_arg(const Engine* e, int M, int N, int K) { return e->bf ? 0 : split_for(M, N, K); }
+
 // LoRA operand: bf16 shadow in bf16 mode, fp32 master otherwise
 static Operand lora_op(const Engine* e, const DenseRef& t, bool kmode, int64_t ld) {
   if (e->bf && t.bf) return Operand{kmode ? SRC_BF16_K : SRC_BF16_R, t.bf, nullptr, ld};
@@ -353,7 +356,7 @@ static int proj_forward(Engine* e, int l, int p, const void* x, void* y, int y_b
     u.A = act_k(e, x, In);
     u.B = lora_op(e, w.la[p], false, nr);
     u.C = e->sv[l].u[p]; u.ldc = nr; u.c_bf16 = e->bf;
-    u.split_k = split_for(T, nr, In);
+    u.split_k = split_arg(e, T, nr, In);
     if (int rc = gemm(u, s)) return rc;
     g.K2 = nr;
     g.A2 = act_k(e, e->sv[l].u[p], nr);
@@ -361,7 +364,7 @@ static int proj_forward(Engine* e, int l, int p, const void* x, void* y, int y_b
     g.alpha2 = lora_scale(e);
   }
   g.M = T; g.N = Out; g.K = In;
-  g.split_k = split_for(T, Out, In);
+  g.split_k = split_arg(e, T, Out, In);
   g.A = act_k(e, x, In);
   g.B = w_fwd(e, w, p);
   g.C = y; g.ldc = Out; g.c_bf16 = y_bf16;
@@ -389,7 +392,7 @@ static int proj_backward(Engine* e, int l, int p, const void* dY, const float* d
     z.A = act_k(e, dY, Out);
     z.B = lora_op(e, w.lb[p], true, Out);
     z.C = e->z; z.ldc = nr; z.c_bf16 = e->bf;
-    z.split_k = split_for(T, nr, Out);
+    z.split_k = split_arg(e, T, nr, Out);
     if (int rc = gemm(z, s)) return rc;
     // dB += s u^T dY   [nr, Out]
     GemmArgs gb{};
@@ -398,7 +401,7 @@ static int proj_backward(Engine* e, int l, int p, const void* dY, const float* d
     gb.A = act_r(e, e->sv[l].u[p], nr);
     gb.B = act_r(e, dY, Out);
     gb.C = w.lb[p].grad; gb.ldc = Out;
-    gb.split_k = split_for(nr, Out, T);
+    gb.split_k = split_arg(e, nr, Out, T);
     if (int rc = gemm(gb, s)) return rc;
     if (e->nblk[p] > 1) {
       if (p == P_QKV) {
@@ -414,7 +417,7 @@ static int proj_backward(Engine* e, int l, int p, const void* dY, const float* d
     ga.A = act_r(e, x, In);
     ga.B = act_r(e, e->z, nr);
     ga.C = w.la[p].grad; ga.ldc = nr;
-    ga.split_k = split_for(In, nr, T);
+    ga.split_k = split_arg(e, In, nr, T);
     if (int rc = gemm(ga, s)) return rc;
     g.K2 = nr;
     g.A2 = act_k(e, e->z, nr);
@@ -428,7 +431,7 @@ static int proj_backward(Engine* e, int l, int p, const void* dY, const float* d
     gw.A = act_r(e, dY, Out);
     gw.B = act_r(e, x, In);
     gw.C = w.w[p].grad; gw.ldc = In;
-    gw.split_k = split_for(Out, In, T);
+    gw.split_k = split_arg(e, Out, In, T);
     if (int rc = gemm(gw, s)) return rc;
     if (e->c.use_bias) {
       SMHIP_REQUIRE(dY_f32, "engine: bias gradients need fp32 activations");
@@ -436,7 +439,7 @@ static int proj_backward(Engine* e, int l, int p, const void* dY, const float* d
     }
   }
   g.M = T; g.N = In; g.K = Out;
-  g.split_k = split_for(T, In, Out);
+  g.split_k = split_arg(e, T, In, Out);
   g.A = act_k(e, dY, Out);
   g.B = w_bwd(e, w, p);
   g.C = dX_out ? dX_out : (void*)dX; g.ldc = In; g.c_bf16 = dX_bf16;
@@ -509,7 +512,7 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
     else if (e->lora) g.B = Operand{e->emb_q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8_R : SRC_Q4K_R, e->emb_q.qs, e->emb_q.sc, d};
     else g.B = e->emb.bf ? Operand{SRC_BF16_R, e->emb.bf, nullptr, d} : Operand{SRC_F32_R, e->emb.data, nullptr, d};
     g.C = e->dx; g.ldc = d;
-    g.split_k = split_for(T, d, V);
+    g.split_k = split_arg(e, T, d, V);
     R_(gemm(g, s));
     if (!e->lora) {
       GemmArgs gw{};
@@ -518,7 +521,7 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
       gw.A = act_r(e, e->dlogits, V);
       gw.B = act_r(e, e->xnf, d);
       gw.C = e->emb.grad; gw.ldc = d;
-      gw.split_k = split_for(V, d, T);
+      gw.split_k = split_arg(e, V, d, T);
       R_(gemm(gw, s));
     }
   }

@@ -456,8 +456,10 @@ __global__ void splitk_epilogue_kernel(const float* __restrict__ partial, int sp
 }
 
 // ---------------------------------------------------------------- host dispatch
-// 256x256 runs 8 waves (2 x 4, each 128 x 64); the others 4 waves.
-enum TileId { T256x256 = 0, T256x128 = 1, T128x128 = 2, T256x64 = 3, NTILE = 4 };
+// 256x256 runs 8 waves (2 x 4, each 128 x 64); the others 4 waves.  64x128 and 128x64 are
+// for skinny products (LoRA rank on one side), which are bandwidth-bound: many small
+// workgroups plus split-K keep every CU streaming.
+enum TileId { T256x256 = 0, T256x128 = 1, T128x128 = 2, T256x64 = 3, T64x128 = 4, T128x64 = 5, NTILE = 6 };
 struct TileInfo { int bm, bn, occ; double eff; };
 // eff: relative MFMA throughput per CU of the tile shape (larger tiles re-read less LDS/L2)
 static const TileInfo kTiles[NTILE] = {
@@ -465,6 +467,8 @@ static const TileInfo kTiles[NTILE] = {
     {256, 128, Shape<256, 128, 2, 4>::OCC, 0.69},  //                         673
     {128, 128, Shape<128, 128, 2, 4>::OCC, 0.88},  //                         856
     {256, 64, Shape<256, 64, 4, 4>::OCC, 0.60},
+    {64, 128, Shape<64, 128, 1, 4>::OCC, 0.50},
+    {128, 64, Shape<128, 64, 4, 4>::OCC, 0.50},
 };
 
 template <int BM, int BN, int WGM, int NW, int AM, int BMD>
@@ -480,7 +484,9 @@ static void launch_tile(int tile, const Args& a, int c_bf16, int sp, hipStream_t
     case T256x256: launch_c<256, 256, 2, 8, AM, BMD>(a, c_bf16, sp, s); break;
     case T256x128: launch_c<256, 128, 2, 4, AM, BMD>(a, c_bf16, sp, s); break;
     case T128x128: launch_c<128, 128, 2, 4, AM, BMD>(a, c_bf16, sp, s); break;
-    default: launch_c<256, 64, 4, 4, AM, BMD>(a, c_bf16, sp, s); break;
+    case T256x64: launch_c<256, 64, 4, 4, AM, BMD>(a, c_bf16, sp, s); break;
+    case T64x128: launch_c<64, 128, 1, 4, AM, BMD>(a, c_bf16, sp, s); break;
+    default: launch_c<128, 64, 4, 4, AM, BMD>(a, c_bf16, sp, s); break;
   }
 }
 
@@ -505,16 +511,19 @@ static bool dispatch(int tile, const Args& a, int amode, int bmode, int c_bf16, 
 
 // pick the tile shape with the smallest estimated time: whole "rounds" of resident
 // workgroups times the per-tile work divided by the shape's efficiency
+static bool skinny(int M, int N) { return M <= 64 || N <= 64; }
 static int pick_tile(int M, int N, int splits, int bmode) {
-  static const int forced = [] {  // SMHIP_GEMM_TILE=0..3 pins the tile shape (tuning runs)
+  static const int forced = [] {  // SMHIP_GEMM_TILE=0..5 pins the tile shape (tuning runs)
     const char* v = getenv("SMHIP_GEMM_TILE");
     return v ? atoi(v) : -1;
   }();
   if (forced >= 0 && forced < NTILE && !(forced == T256x64 && N > 64)) return forced;
+  if (M <= 64) return T64x128;
+  if (N <= 64) return T128x64;
   const int cus = num_cus();
   int best = T128x128;
   double best_t = 1e300;
-  for (int t = 0; t < NTILE; t++) {
+  for (int t = 0; t < T64x128; t++) {
     const TileInfo& ti = kTiles[t];
     if (t == T256x64 && N > 64) continue;
     const int64_t tiles = (int64_t)ceil_div(M, ti.bm) * ceil_div(N, ti.bn) * splits;
@@ -587,9 +596,27 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   a.bias = g.bias; a.R = g.R; a.ldr = g.ldr;
   const int nk = g.K / BK;
   int sp = std::max(1, std::min(g.split_k, nk));
-  a.kps = ceil_div(nk, sp);
-  sp = ceil_div(nk, a.kps);
-  const int tile = pick_tile(g.M, g.N, sp, bm);
+  int tile;
+  if (g.split_k <= 0) {
+    // automatic split-K: fill the machine (2 workgroups per CU slot for skinny, bandwidth-bound
+    // products), keep >= 8 (skinny: 2) K tiles per split and the partials under 64 MiB
+    tile = pick_tile(g.M, g.N, 1, bm);
+    const bool sk = skinny(g.M, g.N);
+    const int64_t tiles = (int64_t)ceil_div(g.M, kTiles[tile].bm) * ceil_div(g.N, kTiles[tile].bn);
+    const int64_t target = (int64_t)num_cus() * kTiles[tile].occ * (sk ? 2 : 1);
+    sp = 1;
+    if (tiles < target) {
+      sp = (int)std::min<int64_t>((target + tiles - 1) / tiles, nk / (sk ? 2 : 8));
+      sp = std::max(1, std::min(sp, 64));
+      while (sp > 1 && (int64_t)sp * g.M * g.N * 4 > ((int64_t)64 << 20)) sp--;
+    }
+    a.kps = ceil_div(nk, sp);
+    sp = ceil_div(nk, a.kps);
+  } else {
+    a.kps = ceil_div(nk, sp);
+    sp = ceil_div(nk, a.kps);
+    tile = pick_tile(g.M, g.N, sp, bm);
+  }
   a.tiles_m = ceil_div(g.M, kTiles[tile].bm);
   a.tiles_n = ceil_div(g.N, kTiles[tile].bn);
   a.partial = nullptr;
