@@ -163,11 +163,203 @@ __global__ void colsum_add2_kernel(const float* __restrict__ part, float* __rest
   *dst += s;
 }
 
+// ---------------------------------------------------------------- vectorised form, D = 64 / 128
+// Half a wave (32 lanes) per (token, head) row, E = D/32 consecutive elements per lane, two
+// rows per wave.  NeoX rotation partners (d, d + D/2) sit 16 lanes apart in the same half
+// (__shfl_xor 16); adjacent pairs (2p, 2p+1) sit in one lane.  Same arithmetic per element
+// as the generic kernels above; the sum of squares / dot products reduce in a different order.
+template <int E> struct VecF;
+template <> struct VecF<2> { typedef float2 T; };
+template <> struct VecF<4> { typedef float4 T; };
+template <int E> __device__ __forceinline__ void ldE(const float* p, float* v) {
+  const typename VecF<E>::T t = *reinterpret_cast<const typename VecF<E>::T*>(p);
+  const float* f = reinterpret_cast<const float*>(&t);
+#pragma unroll
+  for (int i = 0; i < E; i++) v[i] = f[i];
+}
+template <int E, typename TA> __device__ __forceinline__ void stE(TA* p, const float* v) {
+  if constexpr (sizeof(TA) == 4) {
+    typename VecF<E>::T t;
+    float* f = reinterpret_cast<float*>(&t);
+#pragma unroll
+    for (int i = 0; i < E; i++) f[i] = v[i];
+    *reinterpret_cast<typename VecF<E>::T*>(p) = t;
+  } else {
+    uint32_t w[E / 2];
+#pragma unroll
+    for (int i = 0; i < E / 2; i++) w[i] = pack_bf2(v[2 * i], v[2 * i + 1]);
+    if constexpr (E == 4) *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+    else *reinterpret_cast<uint32_t*>(p) = w[0];
+  }
+}
+__device__ __forceinline__ float half_sum(float v) {
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+template <int D, typename TA>
+__global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
+    const float* __restrict__ qkv, TA* __restrict__ qo, TA* __restrict__ ko, TA* __restrict__ vo,
+    float* __restrict__ rinv, const float* __restrict__ wq, const float* __restrict__ wk,
+    const float* __restrict__ cosT, const float* __restrict__ sinT, int T, int S, int Hq, int Hkv,
+    int qk_norm, int neox, float eps) {
+  constexpr int E = D / 32, P = D / 2;
+  const int l = threadIdx.x & 31;
+  const int H = Hq + 2 * Hkv, nqkv = H * D;
+  const int64_t rows = (int64_t)T * H;
+  const int64_t r0 = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  // every lane of a half-wave shares the row; both halves of a wave stay in the loop
+  // together (trip counts differ by at most one, handled by the row guard)
+  for (int64_t r = r0; r - (threadIdx.x >> 5 & 1) < rows; r += (int64_t)gridDim.x * 8) {
+    const bool live = r < rows;
+    const int64_t rr = live ? r : rows - 1;
+    const int t = (int)(rr / H), hh = (int)(rr % H);
+    const float* x = qkv + (int64_t)t * nqkv + hh * D + l * E;
+    float v[E];
+    ldE<E>(x, v);
+    if (hh >= Hq + Hkv) {
+      if (live) stE<E>(vo + (int64_t)t * Hkv * D + (hh - Hq - Hkv) * D + l * E, v);
+      continue;
+    }
+    const bool isq = hh < Hq;
+    const float* w = (isq ? wq : wk) + l * E;
+    float ri = 1.f;
+    if (qk_norm) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < E; i++) ss += v[i] * v[i];
+      ss = half_sum(ss);
+      ri = 1.f / sqrtf(ss / (float)D + eps);
+      if (live && l == 0) rinv[(int64_t)t * (Hq + Hkv) + hh] = ri;
+#pragma unroll
+      for (int i = 0; i < E; i++) v[i] = v[i] * ri * w[i];
+    }
+    const int pos = t % S;
+    float o[E];
+    if (neox) {
+      const bool lo = l * E < P;
+#pragma unroll
+      for (int i = 0; i < E; i++) {
+        const int p = (l * E + i) % P;
+        const float c = cosT[(int64_t)pos * P + p], sn = sinT[(int64_t)pos * P + p];
+        const float partner = __shfl_xor(v[i], 16, 64);
+        o[i] = lo ? v[i] * c - partner * sn : v[i] * c + partner * sn;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < E; i += 2) {
+        const int p = (l * E + i) / 2;
+        const float c = cosT[(int64_t)pos * P + p], sn = sinT[(int64_t)pos * P + p];
+        o[i] = v[i] * c - v[i + 1] * sn;
+        o[i + 1] = v[i + 1] * c + v[i] * sn;
+      }
+    }
+    if (live) stE<E>((isq ? qo + (int64_t)t * Hq * D + hh * D : ko + (int64_t)t * Hkv * D + (hh - Hq) * D) + l * E, o);
+  }
+}
+
+template <int D, typename TA>
+__global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
+    const float* __restrict__ dq, const float* __restrict__ dk, const float* __restrict__ dv,
+    const float* __restrict__ qkv, const float* __restrict__ rinv, const float* __restrict__ wq,
+    const float* __restrict__ wk, const float* __restrict__ cosT, const float* __restrict__ sinT,
+    TA* __restrict__ dqkv, float* __restrict__ part, int T, int S, int Hq, int Hkv, int qk_norm, int neox) {
+  constexpr int E = D / 32, P = D / 2;
+  const int l = threadIdx.x & 31, hw = threadIdx.x >> 5;  // half-wave 0..7
+  const int H = Hq + 2 * Hkv, nqkv = H * D;
+  const int64_t rows = (int64_t)T * H;
+  float aq[E], ak[E];
+#pragma unroll
+  for (int i = 0; i < E; i++) { aq[i] = 0.f; ak[i] = 0.f; }
+  for (int64_t r = (int64_t)blockIdx.x * 8 + hw; r - (hw & 1) < rows; r += (int64_t)gridDim.x * 8) {
+    const bool live = r < rows;
+    const int64_t rr = live ? r : rows - 1;
+    const int t = (int)(rr / H), hh = (int)(rr % H);
+    TA* dst = dqkv + (int64_t)t * nqkv + hh * D + l * E;
+    float g[E];
+    if (hh >= Hq + Hkv) {
+      ldE<E>(dv + (int64_t)t * Hkv * D + (hh - Hq - Hkv) * D + l * E, g);
+      if (live) stE<E>(dst, g);
+      continue;
+    }
+    const bool isq = hh < Hq;
+    ldE<E>((isq ? dq + (int64_t)t * Hq * D + hh * D : dk + (int64_t)t * Hkv * D + (hh - Hq) * D) + l * E, g);
+    const int pos = t % S;
+    float gr[E];
+    if (neox) {
+      const bool lo = l * E < P;
+#pragma unroll
+      for (int i = 0; i < E; i++) {
+        const int p = (l * E + i) % P;
+        const float c = cosT[(int64_t)pos * P + p], sn = sinT[(int64_t)pos * P + p];
+        const float partner = __shfl_xor(g[i], 16, 64);
+        gr[i] = lo ? c * g[i] + sn * partner : -sn * partner + c * g[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < E; i += 2) {
+        const int p = (l * E + i) / 2;
+        const float c = cosT[(int64_t)pos * P + p], sn = sinT[(int64_t)pos * P + p];
+        gr[i] = c * g[i] + sn * g[i + 1];
+        gr[i + 1] = -sn * g[i] + c * g[i + 1];
+      }
+    }
+    if (!qk_norm) {
+      if (live) stE<E>(dst, gr);
+      continue;
+    }
+    float x[E];
+    ldE<E>(qkv + (int64_t)t * nqkv + hh * D + l * E, x);
+    const float* w = (isq ? wq : wk) + l * E;
+    const float ri = rinv[(int64_t)t * (Hq + Hkv) + hh];
+    float dot = 0.f, xn[E];
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      xn[i] = x[i] * ri;
+      dot += gr[i] * w[i] * xn[i];
+      if (live) {
+        if (isq) aq[i] += gr[i] * xn[i];
+        else ak[i] += gr[i] * xn[i];
+      }
+    }
+    dot = half_sum(dot) / (float)D;
+    float o[E];
+#pragma unroll
+    for (int i = 0; i < E; i++) o[i] = ri * (gr[i] * w[i] - xn[i] * dot);
+    if (live) stE<E>(dst, o);
+  }
+  if (part) {  // block partial of dw: sum the 8 half-waves in a fixed order
+    __shared__ float sh[8][2][D];
+#pragma unroll
+    for (int i = 0; i < E; i++) {
+      sh[hw][0][l * E + i] = aq[i];
+      sh[hw][1][l * E + i] = ak[i];
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < 2 * D; c += 256) {
+      float acc = 0.f;
+      for (int h = 0; h < 8; h++) acc += sh[h][c / D][c % D];
+      part[(int64_t)blockIdx.x * 2 * D + c] = acc;
+    }
+  }
+}
+
 int qkv_prep_forward(const float* qkv, void* q, void* k, void* v, float* rinv, const float* wq,
                      const float* wk, const float* cosT, const float* sinT, int T, int S, int Hq, int Hkv,
                      int D, int qk_norm, int neox, float eps, int bf16, hipStream_t s) {
   SMHIP_REQUIRE(D <= 128 && D % 2 == 0, "qkv prep: head_dim must be even and <= 128");
   const int64_t rows = (int64_t)T * (Hq + 2 * Hkv);
+  if (D == 128 || D == 64) {
+    const int gv = gridn(rows, 8);
+#define SMHIP_QKV_FWD(DD, TT) \
+  hipLaunchKernelGGL((qkv_prep_fwd_vec_kernel<DD, TT>), dim3(gv), dim3(256), 0, s, qkv, (TT*)q, (TT*)k, (TT*)v, rinv, wq, wk, cosT, sinT, T, S, Hq, Hkv, qk_norm, neox, eps)
+    if (D == 128) { if (bf16) SMHIP_QKV_FWD(128, uint16_t); else SMHIP_QKV_FWD(128, float); }
+    else { if (bf16) SMHIP_QKV_FWD(64, uint16_t); else SMHIP_QKV_FWD(64, float); }
+#undef SMHIP_QKV_FWD
+    SMHIP_CHECK_LAUNCH();
+    return SMHIP_OK;
+  }
   const int g = gridn(rows, 4);
   if (bf16)
     hipLaunchKernelGGL(qkv_prep_fwd_kernel<uint16_t>, dim3(g), dim3(256), 0, s, qkv, (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, rinv, wq, wk, cosT, sinT, T, S, Hq, Hkv, D, qk_norm, neox, eps);
@@ -183,13 +375,22 @@ int qkv_prep_backward(const float* dq, const float* dk, const float* dv, const f
                       int neox, int bf16, hipStream_t s) {
   SMHIP_REQUIRE(D <= 128 && D % 2 == 0, "qkv prep: head_dim must be even and <= 128");
   const int64_t rows = (int64_t)T * (Hq + 2 * Hkv);
-  const int g = gridn(rows, 4, 2);
+  const bool want_dw = qk_norm && (dwq || dwk);
+  const bool vec = D == 128 || D == 64;
+  // dw partials: one row of 2*D per block, so fewer (larger) blocks when they are needed
+  const int g = vec ? gridn(rows, 8, want_dw ? 2 : 8) : gridn(rows, 4, 2);
   float* part = nullptr;
-  if (qk_norm && (dwq || dwk)) {
+  if (want_dw) {
     part = (float*)workspace(s, sizeof(float) * (size_t)g * 2 * D, 7);
     if (!part) return fail(SMHIP_ENOMEM, "qkv prep backward: workspace");
   }
-  if (bf16)
+  if (vec) {
+#define SMHIP_QKV_BWD(DD, TT) \
+  hipLaunchKernelGGL((qkv_prep_bwd_vec_kernel<DD, TT>), dim3(g), dim3(256), 0, s, dq, dk, dv, qkv, rinv, wq, wk, cosT, sinT, (TT*)dqkv, part, T, S, Hq, Hkv, qk_norm, neox)
+    if (D == 128) { if (bf16) SMHIP_QKV_BWD(128, uint16_t); else SMHIP_QKV_BWD(128, float); }
+    else { if (bf16) SMHIP_QKV_BWD(64, uint16_t); else SMHIP_QKV_BWD(64, float); }
+#undef SMHIP_QKV_BWD
+  } else if (bf16)
     hipLaunchKernelGGL(qkv_prep_bwd_kernel<uint16_t>, dim3(g), dim3(256), 0, s, dq, dk, dv, qkv, rinv, wq, wk, cosT, sinT, (uint16_t*)dqkv, part, T, S, Hq, Hkv, D, qk_norm, neox);
   else
     hipLaunchKernelGGL(qkv_prep_bwd_kernel<float>, dim3(g), dim3(256), 0, s, dq, dk, dv, qkv, rinv, wq, wk, cosT, sinT, (float*)dqkv, part, T, S, Hq, Hkv, D, qk_norm, neox);

@@ -115,6 +115,15 @@ def test_engine_lora_fp32(orc, dev, qtype):
     run_pair(orc, dev, c, seed=5)
 
 
+@pytest.mark.parametrize("neox", [0, 1])
+def test_engine_full_fp32_head128(orc, dev, neox):
+    """head_dim 128 (the vectorised QK-norm/RoPE kernels) with both RoPE pairings and the
+    q_norm / k_norm weight gradients, fp32 mode."""
+    c = ModelConfig(n_layers=1, d_model=256, n_heads=2, n_kv_heads=1, head_dim=128, ffn_dim=256, vocab=256, batch=2,
+                    seq=64, rope_theta=1e6, rope_neox=neox, qk_norm=1)
+    run_pair(orc, dev, c, seed=11 + neox)
+
+
 @pytest.mark.parametrize("qtype", [QTYPE_Q8_0, QTYPE_Q4_K])
 def test_engine_lora_bf16(orc, dev, qtype):
     c = ModelConfig(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=512, batch=2,
