@@ -682,6 +682,82 @@ __global__ __launch_bounds__(NT) void ce_rows_2pass_kernel(
   }
 }
 
+// Two-pass rows, float4 (V % 4 == 0, 16-byte aligned rows): pass 1 folds 4 logits per online
+// (max, sum-exp) update, pass 2 writes 4 gradients per lane.  bf16 output (the training
+// engine's bf16 mode) uses the hardware exp2 (__expf); fp32 output keeps expf.
+template <typename TOut>
+__device__ __forceinline__ float ce_exp(float x) {
+  if constexpr (sizeof(TOut) == 2) return __expf(x);
+  else return expf(x);
+}
+template <int NT, typename TOut>
+__global__ __launch_bounds__(NT) void ce_rows_2pass_vec_kernel(
+    const float* __restrict__ logits, const int32_t* __restrict__ labels, TOut* __restrict__ dL,
+    float* __restrict__ row_loss, const int* __restrict__ count, int T, int V, int ignoreId,
+    float smoothing) {
+  __shared__ float shm[2 * NT / 64 + 2 * NT / 64];
+  const int real = *count;
+  const float scale = real > 0 ? 1.f / (float)real : 0.f;
+  const float epsOverV = smoothing / (float)V, oneMinusE = 1.f - smoothing;
+  const int V4 = V / 4;
+  for (int t = blockIdx.x; t < T; t += gridDim.x) {
+    const int lab = labels[t];
+    const float* z = logits + (int64_t)t * V;
+    TOut* d = dL + (int64_t)t * V;
+    if (lab == ignoreId) {
+      for (int c = threadIdx.x; c < V; c += NT) d[c] = (TOut)0;
+      if (threadIdx.x == 0 && row_loss) row_loss[t] = 0.f;
+      continue;
+    }
+    float m = -INFINITY, sum = 0.f, zsum = 0.f;
+    for (int c4 = threadIdx.x; c4 < V4; c4 += NT) {
+      const float4 v = ld4(z + 4 * c4);
+      zsum += (v.x + v.y) + (v.z + v.w);
+      const float mx = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
+      if (mx > m) {
+        sum = sum * ce_exp<TOut>(m - mx);
+        m = mx;
+      }
+      sum += (ce_exp<TOut>(v.x - m) + ce_exp<TOut>(v.y - m)) + (ce_exp<TOut>(v.z - m) + ce_exp<TOut>(v.w - m));
+    }
+    block_max_sum<NT>(m, sum, shm);
+    if (smoothing > 0.f) zsum = block_sum<NT>(zsum, shm + 2 * NT / 64);
+    const float zl = z[lab];
+    __syncthreads();  // z may alias d
+    const float inv = 1.f / sum;
+    for (int c4 = threadIdx.x; c4 < V4; c4 += NT) {
+      const float4 v = ld4(z + 4 * c4);
+      float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        float p = ce_exp<TOut>(e[i] - m) * inv;
+        const int c = 4 * c4 + i;
+        if (smoothing > 0.f) {
+          p -= epsOverV;
+          if (c == lab) p -= oneMinusE;
+        } else if (c == lab) {
+          p -= 1.f;
+        }
+        e[i] = p * scale;
+      }
+      if constexpr (sizeof(TOut) == 4) {
+        st4((float*)(d + 4 * c4), make_float4(e[0], e[1], e[2], e[3]));
+      } else {
+        *reinterpret_cast<uint2*>(d + 4 * c4) = make_uint2(pack_bf2(e[0], e[1]), pack_bf2(e[2], e[3]));
+      }
+    }
+    if (threadIdx.x == 0 && row_loss) {
+      float lp = (zl - m) - logf(sum);
+      if (smoothing <= 0.f) {
+        row_loss[t] = -lp;
+      } else {
+        float slp = zsum - (float)V * m - (float)V * logf(sum);
+        row_loss[t] = -(oneMinusE * lp + epsOverV * slp);
+      }
+    }
+  }
+}
+
 __global__ void mean_loss_kernel(const float* __restrict__ row_loss, const int* __restrict__ count,
                                  int T, float* __restrict__ out) {
   __shared__ double sh[kBlock];
@@ -711,6 +787,8 @@ static int ce_launch(const float* logits, const int32_t* labels, TOut* dL, float
     hipLaunchKernelGGL((ce_rows_reg_kernel<1024, 8, TOut>), dim3(G), dim3(1024), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
   else if (v4 && V <= 256 * 4 * 8)
     hipLaunchKernelGGL((ce_rows_reg_kernel<256, 8, TOut>), dim3(G), dim3(256), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
+  else if (v4)
+    hipLaunchKernelGGL((ce_rows_2pass_vec_kernel<1024, TOut>), dim3(G), dim3(1024), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
   else
     hipLaunchKernelGGL((ce_rows_2pass_kernel<1024, TOut>), dim3(G), dim3(1024), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
   SMHIP_CHECK_LAUNCH();

@@ -132,6 +132,15 @@ def test_engine_lora_bf16(orc, dev, qtype):
     run_pair(orc, dev, c, seed=7, tol=3e-2, loss_tol=2e-2)
 
 
+def test_engine_lora_bf16_large_vocab(orc, dev):
+    """Vocabulary above the register-resident cross-entropy limit (the two-pass row kernel,
+    bf16 output) in a LoRA bf16 step."""
+    c = ModelConfig(n_layers=1, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=256, vocab=40000, batch=1,
+                    seq=128, rope_theta=1e6, rope_neox=1, qk_norm=1, base_qtype=QTYPE_Q8_0, lora_rank=8,
+                    lora_alpha=16.0, precision=PREC_BF16)
+    run_pair(orc, dev, c, seed=13, tol=3e-2, loss_tol=2e-2)
+
+
 def test_engine_full_bf16(orc, dev):
     c = ModelConfig(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=512, batch=2,
                     seq=128, rope_theta=1e6, rope_neox=1, qk_norm=1, precision=PREC_BF16)
