@@ -79,6 +79,51 @@ __device__ inline void stage(const uint16_t* __restrict__ g, int64_t ld, int r0,
   }
 }
 
+// Register-prefetched staging: load() issues the global reads of a [NR][D] row tile (pairs
+// of rows per 16-byte column chunk) into registers, store() writes them to LDS as [NR][D+8]
+// and/or transposed [D][NR+8].  Loading tile t+1 before the MFMAs of tile t hides the
+// global latency behind the compute.
+template <int D, int NR>
+struct Pref {
+  static constexpr int U = (NR / 2) * (D / 8);          // (row pair, chunk) units
+  static constexpr int PER = (U + 255) / 256;
+  uint4 a[PER], b[PER];
+  __device__ inline void load(const uint16_t* __restrict__ g, int64_t ld, int r0) {
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const int c = i * 256 + threadIdx.x;
+      if (c < U) {
+        const int rp = c % (NR / 2), dc = (c / (NR / 2)) * 8;
+        a[i] = *reinterpret_cast<const uint4*>(g + (int64_t)(r0 + 2 * rp) * ld + dc);
+        b[i] = *reinterpret_cast<const uint4*>(g + (int64_t)(r0 + 2 * rp + 1) * ld + dc);
+      }
+    }
+  }
+  template <bool ROWS, bool TRANS>
+  __device__ inline void store(uint16_t* sRow, uint16_t* sT) const {
+    constexpr int RP = D + 8, TP = NR + 8;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const int c = i * 256 + threadIdx.x;
+      if (c >= U) continue;
+      const int rp = c % (NR / 2), dc = (c / (NR / 2)) * 8;
+      if constexpr (ROWS) {
+        *reinterpret_cast<uint4*>(sRow + (2 * rp) * RP + dc) = a[i];
+        *reinterpret_cast<uint4*>(sRow + (2 * rp + 1) * RP + dc) = b[i];
+      }
+      if constexpr (TRANS) {
+        const uint32_t av[4] = {a[i].x, a[i].y, a[i].z, a[i].w}, bv[4] = {b[i].x, b[i].y, b[i].z, b[i].w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const uint32_t lo = (j & 1) ? (av[j >> 1] >> 16) : (av[j >> 1] & 0xFFFFu);
+          const uint32_t hi = (j & 1) ? (bv[j >> 1] >> 16) : (bv[j >> 1] & 0xFFFFu);
+          *reinterpret_cast<uint32_t*>(sT + (dc + j) * TP + 2 * rp) = lo | (hi << 16);
+        }
+      }
+    }
+  }
+};
+
 // ============================================================================
 // forward: grid (S/128, Hq, B), 4 waves x 32 queries, key tiles of 64
 // ============================================================================
@@ -242,12 +287,23 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
   const float* lrow = lse + ((int64_t)b * Hq + h) * S;
   const float* drow = Di + ((int64_t)b * Hq + h) * S;
 
-  for (int q0 = kbk * 128; q0 < S; q0 += QB) {
+  Pref<D, QB> pq, pd;
+  float pl = 0.f, pdi = 0.f;
+  const int qstart = kbk * 128;
+  pq.load(qb_, ldq, qstart);
+  pd.load(db_, lddo, qstart);
+  if (threadIdx.x < QB) { pl = lrow[qstart + threadIdx.x]; pdi = drow[qstart + threadIdx.x]; }
+  for (int q0 = qstart; q0 < S; q0 += QB) {
     __syncthreads();
-    stage<D, QB, true, true>(qb_, ldq, q0, sQ, sQt);
-    stage<D, QB, true, true>(db_, lddo, q0, sdO, sdOt);
-    if (threadIdx.x < QB) { sL[threadIdx.x] = lrow[q0 + threadIdx.x]; sDi[threadIdx.x] = drow[q0 + threadIdx.x]; }
+    pq.template store<true, true>(sQ, sQt);
+    pd.template store<true, true>(sdO, sdOt);
+    if (threadIdx.x < QB) { sL[threadIdx.x] = pl; sDi[threadIdx.x] = pdi; }
     __syncthreads();
+    if (q0 + QB < S) {  // next tile in flight during this tile's MFMAs
+      pq.load(qb_, ldq, q0 + QB);
+      pd.load(db_, lddo, q0 + QB);
+      if (threadIdx.x < QB) { pl = lrow[q0 + QB + threadIdx.x]; pdi = drow[q0 + QB + threadIdx.x]; }
+    }
     if (q0 + QB - 1 < kw0) continue;  // every query precedes this wave's keys
     // S = Q K^T and dP = dO V^T : rows = queries, cols = keys (lane <-> key)
     floatx16 sacc, dpacc;
@@ -327,11 +383,18 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
   const uint16_t* vb = v + (int64_t)b * S * ldv + kvh * D;
   const int kend = (qb + 1) * 128;
   const int wq_last = qb * 128 + w * 32 + 31;
+  Pref<D, KB> pk, pv;
+  pk.load(kb, ldk, 0);
+  pv.load(vb, ldv, 0);
   for (int k0 = 0; k0 < kend; k0 += KB) {
     __syncthreads();
-    stage<D, KB, true, true>(kb, ldk, k0, sK, sKt);
-    stage<D, KB, true, false>(vb, ldv, k0, sV, nullptr);
+    pk.template store<true, true>(sK, sKt);
+    pv.template store<true, false>(sV, nullptr);
     __syncthreads();
+    if (k0 + KB < kend) {
+      pk.load(kb, ldk, k0 + KB);
+      pv.load(vb, ldv, k0 + KB);
+    }
     if (k0 > wq_last) continue;
     // S^T = K Q^T, dP^T = V dO^T : rows = keys, cols = queries (lane <-> query)
     floatx16 s[2], dp[2];
