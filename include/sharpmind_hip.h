@@ -214,6 +214,12 @@ int smhip_engine_forward_backward(void* engine, const int32_t* ids, const int32_
 int smhip_engine_optimizer_step(void* engine, float* grad_norm_sq, smhip_stream_t stream);
 int smhip_engine_step(void* engine, const int32_t* ids, const int32_t* labels, float* loss,
                       smhip_stream_t stream);
+/* Execution mode of forward_backward (no reference counterpart: the reference runs on the
+ * CPU).  on != 0: the first call records the step's ~1500 kernel launches as a HIP graph on a
+ * private stream (after one eager pass that also produces that call's result), later calls copy
+ * ids/labels into engine buffers and replay the graph on the caller's stream.  Results are
+ * bit-identical to eager mode.  Calls made while the live profiler is active run eagerly. */
+int smhip_engine_use_graph(void* engine, int on);
 /* Diagnostics: copy a saved activation of the last forward to host memory.  what: "h_in", "h_mid",
  * "xn1", "qkv", "q", "k", "v", "o", "gu", "act" (of `layer`), "h_fin", "logits" ("logits" holds
  * dLogits after a fp32-mode backward).  Element type is bf16 for "xn1|q|k|v|o|gu|act" in bf16

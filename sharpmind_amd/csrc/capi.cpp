@@ -80,6 +80,7 @@ int prof_mark(hipStream_t s) {
   hipEventRecord(p->ev[p->used], s);
   return (int)p->used++;
 }
+bool profiling_active() { return g_prof != nullptr; }
 void prof_add(int cat, int i0, int i1, double flops, int M, int N, int K) {
   if (g_prof && i0 >= 0 && i1 >= 0) g_prof->recs.push_back({cat, i0, i1, flops, M, N, K});
 }

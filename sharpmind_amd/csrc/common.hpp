@@ -170,6 +170,7 @@ int gemm(const GemmArgs& g, hipStream_t s);
 // HIP events on the launch stream; smhip_profile_end sums the elapsed times.
 enum ProfCat { PROF_GEMM = 0, PROF_FLASH_FWD = 1, PROF_FLASH_BWD = 2, PROF_NCAT = 3 };
 int prof_mark(hipStream_t s);                         // -1 when profiling is off
+bool profiling_active();
 void prof_add(int cat, int i0, int i1, double flops, int M = 0, int N = 0, int K = 0);
 
 }  // namespace smhip

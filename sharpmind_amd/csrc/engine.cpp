@@ -80,6 +80,11 @@ struct Engine {
   void *dh_ta, *dgu, *dO, *dqkv, *z;
   void* flash_ws = nullptr;
   int step = 0;
+  // graph mode: forward_backward recorded once as a HIP graph on a private stream and replayed
+  bool use_graph = false;
+  hipStream_t cap = nullptr;
+  hipGraphExec_t gexec = nullptr;
+  int32_t *ids_in = nullptr, *labels_in = nullptr;  // engine-owned inputs the graph reads
 };
 
 static inline void* dalloc(Engine* e, size_t bytes) {
@@ -259,7 +264,9 @@ static int build(Engine* e) {
   e->z = dalloc(e, ES * (size_t)T * std::max(3 * r, 1));
   (void)wmax;
   if (e->bf) e->flash_ws = dalloc(e, flash_backward_workspace(c.batch, c.seq, c.n_heads, c.head_dim));
-  if (!e->dh || !e->dgu || !e->dqkv || !e->logits || !e->dlogits || (e->bf && !e->flash_ws))
+  e->ids_in = (int32_t*)dalloc(e, sizeof(int32_t) * (size_t)T);
+  e->labels_in = (int32_t*)dalloc(e, sizeof(int32_t) * (size_t)T);
+  if (!e->ids_in || !e->labels_in || !e->dh || !e->dgu || !e->dqkv || !e->logits || !e->dlogits || (e->bf && !e->flash_ws))
     return fail(SMHIP_ENOMEM, "engine: work buffers");
 
   // RoPE tables (host, RoPE.cs:99-148)
@@ -627,6 +634,8 @@ int smhip_engine_destroy(void* engine) {
   if (!engine) return SMHIP_OK;
   Engine* e = (Engine*)engine;
   hipDeviceSynchronize();
+  if (e->gexec) hipGraphExecDestroy(e->gexec);
+  if (e->cap) hipStreamDestroy(e->cap);
   for (void* p : e->allocs) hipFree(p);
   delete e;
   return SMHIP_OK;
@@ -838,11 +847,57 @@ int smhip_engine_init_synthetic(void* engine, uint64_t seed) {
   return hipDeviceSynchronize() == hipSuccess ? SMHIP_OK : fail(SMHIP_EHIP, "init_synthetic");
 }
 
+int smhip_engine_use_graph(void* engine, int on) {
+  SMHIP_REQUIRE(engine, "engine: null handle");
+  Engine* e = (Engine*)engine;
+  e->use_graph = on != 0;
+  return SMHIP_OK;
+}
+
+// Graph mode.  The first call runs forward_backward eagerly on the engine's private stream
+// (so every workspace the step needs is allocated, keyed to that stream), then records the
+// same sequence as a graph; later calls copy the inputs into engine buffers and launch the
+// graph on the caller's stream.  Every kernel is deterministic, so a replay produces the same
+// bits as the eager step.  The live profiler (smhip_profile_begin) needs eager launches, so a
+// call while it is active runs eagerly.
+static int forward_backward_graph(Engine* e, const int32_t* ids, const int32_t* labels, hipStream_t s) {
+  const size_t bytes = sizeof(int32_t) * (size_t)e->T;
+  SMHIP_CHECK_HIP(hipMemcpyAsync(e->ids_in, ids, bytes, hipMemcpyDeviceToDevice, s));
+  SMHIP_CHECK_HIP(hipMemcpyAsync(e->labels_in, labels, bytes, hipMemcpyDeviceToDevice, s));
+  if (e->gexec) {
+    SMHIP_CHECK_HIP(hipGraphLaunch(e->gexec, s));
+    return SMHIP_OK;
+  }
+  if (!e->cap) SMHIP_CHECK_HIP(hipStreamCreateWithFlags(&e->cap, hipStreamNonBlocking));
+  SMHIP_CHECK_HIP(hipStreamSynchronize(s));
+  int rc = forward_backward(e, e->ids_in, e->labels_in, e->cap);  // this step's result + workspaces
+  if (rc) return rc;
+  SMHIP_CHECK_HIP(hipStreamSynchronize(e->cap));
+  SMHIP_CHECK_HIP(hipStreamBeginCapture(e->cap, hipStreamCaptureModeThreadLocal));
+  rc = forward_backward(e, e->ids_in, e->labels_in, e->cap);
+  hipGraph_t g = nullptr;
+  const hipError_t ec = hipStreamEndCapture(e->cap, &g);
+  if (rc) {
+    if (g) hipGraphDestroy(g);
+    return rc;
+  }
+  if (ec != hipSuccess || !g) return fail(SMHIP_EHIP, "engine: graph capture failed");
+  const hipError_t ei = hipGraphInstantiate(&e->gexec, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  if (ei != hipSuccess) {
+    e->gexec = nullptr;
+    return fail(SMHIP_EHIP, "engine: graph instantiation failed");
+  }
+  return SMHIP_OK;
+}
+
 int smhip_engine_forward_backward(void* engine, const int32_t* ids, const int32_t* labels, float* loss,
                                   smhip_stream_t stream) {
   SMHIP_REQUIRE(engine && ids && labels, "engine_forward_backward: null argument");
   Engine* e = (Engine*)engine;
-  int rc = forward_backward(e, ids, labels, (hipStream_t)stream);
+  int rc;
+  if (e->use_graph && !profiling_active()) rc = forward_backward_graph(e, ids, labels, (hipStream_t)stream);
+  else rc = forward_backward(e, ids, labels, (hipStream_t)stream);
   if (rc) return rc;
   if (loss) SMHIP_CHECK_HIP(hipMemcpyAsync(loss, e->loss, sizeof(float), hipMemcpyDeviceToDevice, (hipStream_t)stream));
   return SMHIP_OK;

@@ -80,6 +80,10 @@ class Engine:
         check(lib().smhip_engine_optimizer_step(self.h, grad_norm_sq.data_ptr() if grad_norm_sq is not None else None,
                                                 self._stream()))
 
+    def use_graph(self, on=True):
+        """Replay forward_backward as a recorded HIP graph (bit-identical to eager launches)."""
+        check(lib().smhip_engine_use_graph(self.h, 1 if on else 0))
+
     def step(self, ids, labels, loss=None):
         check(lib().smhip_engine_step(self.h, ids.data_ptr(), labels.data_ptr(),
                                       loss.data_ptr() if loss is not None else None, self._stream()))

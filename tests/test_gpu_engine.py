@@ -233,3 +233,35 @@ def test_device_encoder_bitexact(orc, dev, qtype):
                                                            torch.cuda.current_stream().cuda_stream))
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy(), raw_ref)
+
+
+def test_engine_graph_replay_matches_eager(orc, dev):
+    """Graph mode: the recorded step replayed several times, with unrelated eager work and
+    synchronisations in between, gives gradients and loss bit-identical to eager launches."""
+    c = ModelConfig(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=512, batch=2,
+                    seq=128, rope_theta=1e6, rope_neox=1, qk_norm=1, base_qtype=QTYPE_Q8_0, lora_rank=8,
+                    lora_alpha=16.0, precision=PREC_BF16)
+    eng, P, G = build(orc, c, 21)
+    rng = np.random.default_rng(22)
+    batches = [torch.from_numpy(rng.integers(0, c.vocab, c.tokens).astype(np.int32)).to(dev) for _ in range(2)]
+    loss = torch.zeros(1, device=dev)
+
+    def grads():
+        return {n: eng.get(n, g.shape, grad=True) for n, g in G.items()}
+
+    ref = []
+    for ids in batches:  # eager
+        eng.forward_backward(ids, next_token_labels(ids, c.seq), loss)
+        torch.cuda.synchronize()
+        ref.append((float(loss.cpu()[0]), grads()))
+    eng.use_graph(True)
+    for rep in range(3):
+        for i, ids in enumerate(batches):
+            scratch = torch.randn(1 << 20, device=dev)  # unrelated eager work between replays
+            scratch.mul_(2.0).sum().item()
+            eng.forward_backward(ids, next_token_labels(ids, c.seq), loss)
+            torch.cuda.synchronize()
+            assert float(loss.cpu()[0]) == ref[i][0], (rep, i)
+            got = grads()
+            for n in got:
+                assert np.array_equal(got[n], ref[i][1][n]), (rep, i, n)
