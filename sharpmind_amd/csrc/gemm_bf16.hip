@@ -277,9 +277,61 @@ __device__ __forceinline__ void gen_tile(int mode, const Op& o, int r0, int k0, 
   }
 }
 
+// Vectorised rank-extension staging for bf16 operands whose rank K2 and row length are
+// multiples of 8 with 16-byte aligned rows: whole 8-element chunks (k-contiguous) or 8 x 8
+// register transposes (row-contiguous); chunks at k >= K2 are zero.  Same values as gen_tile.
+__device__ __forceinline__ uint4 scale_bf8(uint4 v, float mult) {
+  if (mult == 1.f) return v;
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) o[i] = pk(mult * bf2f((uint16_t)(w[i] & 0xFFFFu)), mult * bf2f((uint16_t)(w[i] >> 16)));
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+template <int ROWS, int NT>
+__device__ __forceinline__ void ext_tile_k(const Op& o, int r0, int k0, int R, int K, float mult, uint8_t* lds) {
+  const uint16_t* p = (const uint16_t*)o.p;
+  for (int c = threadIdx.x; c < ROWS * 8; c += NT) {
+    const int r = c >> 3, ch = c & 7, k = k0 + ch * 8;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (r0 + r < R && k < K) v = scale_bf8(*reinterpret_cast<const uint4*>(p + (int64_t)(r0 + r) * o.ld + k), mult);
+    *reinterpret_cast<uint4*>(lds + sw(r, ch)) = v;
+  }
+}
+template <int ROWS, int NT>
+__device__ __forceinline__ void ext_tile_r(const Op& o, int r0, int k0, int R, int K, float mult, uint8_t* lds) {
+  const uint16_t* p = (const uint16_t*)o.p;
+  for (int c = threadIdx.x; c < ROWS; c += NT) {  // (8-row group, 8-k chunk)
+    const int rg = c % (ROWS / 8), ch = c / (ROWS / 8), kb = k0 + ch * 8;
+    uint32_t w[8][4];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (kb + j < K && r0 + rg * 8 < R) v = *reinterpret_cast<const uint4*>(p + (int64_t)(kb + j) * o.ld + r0 + rg * 8);
+      w[j][0] = v.x; w[j][1] = v.y; w[j][2] = v.z; w[j][3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {  // row rg*8+i: k = kb..kb+7
+      uint32_t e[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) e[j] = (i & 1) ? (w[j][i >> 1] >> 16) : (w[j][i >> 1] & 0xFFFFu);
+      uint4 v = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
+      *reinterpret_cast<uint4*>(lds + sw(rg * 8 + i, ch)) = scale_bf8(v, mult);
+    }
+  }
+}
+template <int ROWS, int NT>
+__device__ __forceinline__ void ext_tile(int mode, bool vec, const Op& o, int r0, int k0, int R, int K, float mult,
+                                         uint8_t* lds) {
+  if (vec && mode == SRC_BF16_K) ext_tile_k<ROWS, NT>(o, r0, k0, R, K, mult, lds);
+  else if (vec && mode == SRC_BF16_R) ext_tile_r<ROWS, NT>(o, r0, k0, R, K, mult, lds);
+  else gen_tile<ROWS, NT>(mode, o, r0, k0, R, K, mult, lds);
+}
+
 struct Args {
   Op A, B, A2, B2;
   int amode2, bmode2;
+  int ext_vec;      // extension operands qualify for ext_tile_k / ext_tile_r
   int M, N, K, K2;
   float alpha, alpha2, beta;
   void* C;
@@ -393,8 +445,8 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW>::OCC)) void gemm_k
     }
   }
   for (int t = 0; t < nk2; t++) {  // rank extension (all waves are past the last main-tile barrier)
-    gen_tile<BM, NT>(g.amode2, g.A2, m0, t * BK, g.M, g.K2, g.alpha2, sA(0));
-    gen_tile<BN, NT>(g.bmode2, g.B2, n0, t * BK, g.N, g.K2, 1.f, sB(0));
+    ext_tile<BM, NT>(g.amode2, g.ext_vec != 0, g.A2, m0, t * BK, g.M, g.K2, g.alpha2, sA(0));
+    ext_tile<BN, NT>(g.bmode2, g.ext_vec != 0, g.B2, n0, t * BK, g.N, g.K2, 1.f, sB(0));
     __syncthreads();
     compute(0);
     __syncthreads();
@@ -588,6 +640,16 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   a.B2 = {g.B2.p, g.B2.s, g.B2.ld, 0, 0};
   a.amode2 = g.A2.mode;
   a.bmode2 = g.B2.mode;
+  a.ext_vec = 0;
+  if (g.K2 > 0 && g.K2 % 8 == 0) {
+    bool ok = true;
+    for (const Operand* o : {&g.A2, &g.B2})
+      ok = ok && (o->mode == SRC_BF16_K || o->mode == SRC_BF16_R) && o->ld % 8 == 0 && aligned_16(o->p);
+    // row-contiguous chunks are 8 rows wide: the row count must not end inside one
+    if (g.A2.mode == SRC_BF16_R && g.M % 8) ok = false;
+    if (g.B2.mode == SRC_BF16_R && g.N % 8) ok = false;
+    a.ext_vec = ok ? 1 : 0;
+  }
   a.M = g.M; a.N = g.N; a.K = g.K; a.K2 = g.K2;
   a.alpha = g.alpha;
   a.alpha2 = g.alpha != 0.f ? g.alpha2 / g.alpha : 0.f;
