@@ -483,6 +483,56 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW>::OCC)) void gemm_k
     }
 }
 
+// float4 form (N % 4 == 0, ldc / ldr % 4 == 0): 4 consecutive columns per thread, the
+// partial loads of 8 splits in flight at once; sums still in ascending split order.
+__device__ __forceinline__ void add4(float4& a, const float4& b) { a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w; }
+__global__ void splitk_epilogue4_kernel(const float* __restrict__ partial, int splits, int M, int N, float alpha,
+                                        float beta, void* __restrict__ Cp, int64_t ldc, int c_bf16,
+                                        const float* __restrict__ bias, const float* __restrict__ R, int64_t ldr) {
+  const int64_t n = (int64_t)M * N, n4 = n / 4;
+  for (int64_t i4 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i4 < n4; i4 += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = 4 * i4;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k0 = 0; k0 < splits; k0 += 8) {
+      float4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (k0 + u < splits) v[u] = *reinterpret_cast<const float4*>(partial + (int64_t)(k0 + u) * n + i);
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (k0 + u < splits) add4(acc, v[u]);
+    }
+    const int64_t row = i / N, col = i - row * N;
+    float o[4] = {alpha * acc.x, alpha * acc.y, alpha * acc.z, alpha * acc.w};
+    if (bias) {
+#pragma unroll
+      for (int u = 0; u < 4; u++) o[u] = o[u] + bias[col + u];
+    }
+    if (c_bf16) {
+      uint16_t* c = (uint16_t*)Cp + row * ldc + col;
+      if (beta != 0.f) {
+        const uint2 w = *reinterpret_cast<const uint2*>(c);
+        o[0] = o[0] + beta * bf2f((uint16_t)(w.x & 0xFFFFu));
+        o[1] = o[1] + beta * bf2f((uint16_t)(w.x >> 16));
+        o[2] = o[2] + beta * bf2f((uint16_t)(w.y & 0xFFFFu));
+        o[3] = o[3] + beta * bf2f((uint16_t)(w.y >> 16));
+      }
+      *reinterpret_cast<uint2*>(c) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+    } else {
+      float* c = (float*)Cp + row * ldc + col;
+      if (R) {
+        const float4 r = *reinterpret_cast<const float4*>(R + row * ldr + col);
+        o[0] = o[0] + r.x; o[1] = o[1] + r.y; o[2] = o[2] + r.z; o[3] = o[3] + r.w;
+      }
+      if (beta != 0.f) {
+        const float4 cv = *reinterpret_cast<const float4*>(c);
+        o[0] = o[0] + beta * cv.x; o[1] = o[1] + beta * cv.y; o[2] = o[2] + beta * cv.z; o[3] = o[3] + beta * cv.w;
+      }
+      *reinterpret_cast<float4*>(c) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+  }
+}
+
 // C = alpha * sum_s partial[s] (+ bias) (+ R) (+ beta C); splits summed in ascending order.
 __global__ void splitk_epilogue_kernel(const float* __restrict__ partial, int splits, int M, int N, float alpha,
                                        float beta, void* __restrict__ Cp, int64_t ldc, int c_bf16,
@@ -691,9 +741,16 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   SMHIP_CHECK_LAUNCH();
   prof_add(PROF_GEMM, ev0, prof_mark(s), 2.0 * g.M * g.N * ((double)g.K + g.K2), g.M, g.N, g.K + g.K2);
   if (sp > 1) {
-    const int blocks = (int)std::min<int64_t>(((int64_t)g.M * g.N + 255) / 256, (int64_t)num_cus() * 8);
-    hipLaunchKernelGGL(splitk_epilogue_kernel, dim3(blocks), dim3(256), 0, s, a.partial, sp, g.M, g.N, g.alpha,
-                       g.beta, g.C, g.ldc, g.c_bf16, g.bias, g.R, g.ldr);
+    const bool v4 = g.N % 4 == 0 && g.ldc % 4 == 0 && (!g.R || g.ldr % 4 == 0) && aligned_16(g.C) &&
+                    (!g.R || aligned_16(g.R));
+    const int64_t work = v4 ? (int64_t)g.M * g.N / 4 : (int64_t)g.M * g.N;
+    const int blocks = (int)std::min<int64_t>((work + 255) / 256, (int64_t)num_cus() * 8);
+    if (v4)
+      hipLaunchKernelGGL(splitk_epilogue4_kernel, dim3(blocks), dim3(256), 0, s, a.partial, sp, g.M, g.N, g.alpha,
+                         g.beta, g.C, g.ldc, g.c_bf16, g.bias, g.R, g.ldr);
+    else
+      hipLaunchKernelGGL(splitk_epilogue_kernel, dim3(blocks), dim3(256), 0, s, a.partial, sp, g.M, g.N, g.alpha,
+                         g.beta, g.C, g.ldc, g.c_bf16, g.bias, g.R, g.ldr);
     SMHIP_CHECK_LAUNCH();
   }
   return 1;
