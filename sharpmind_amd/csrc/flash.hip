@@ -248,8 +248,9 @@ __global__ __launch_bounds__(256) void fa_bwd_pre_kernel(const uint16_t* __restr
 }
 
 // ============================================================================
-// backward dK, dV: grid (S/128, Hq, B); 4 waves x 32 keys; query tiles of 32.
-// Writes per-query-head partials dKh/dVh [B, S, Hq, D] fp32.
+// backward dK, dV: grid (S/128, Hq, B); 4 waves x 32 keys; query tiles of QB = 64 (two
+// 32-query MFMA blocks per wave per tile).  Writes per-query-head partials dKh/dVh
+// [B, S, Hq, D] fp32.
 // ============================================================================
 template <int D>
 __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
@@ -257,7 +258,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
     float* __restrict__ dKh, float* __restrict__ dVh, int S, int Hq, int Hkv, int64_t ldq, int64_t ldk,
     int64_t ldv, int64_t lddo, float sl2, float scale) {
-  constexpr int QB = 32, RP = D + 8, TP = QB + 8;
+  constexpr int QB = 64, NQ = QB / 32, RP = D + 8, TP = QB + 8;
   __shared__ __attribute__((aligned(16))) uint16_t sQ[QB * RP];
   __shared__ __attribute__((aligned(16))) uint16_t sQt[D * TP];
   __shared__ __attribute__((aligned(16))) uint16_t sdO[QB * RP];
@@ -305,33 +306,37 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
       if (threadIdx.x < QB) { pl = lrow[q0 + QB + threadIdx.x]; pdi = drow[q0 + QB + threadIdx.x]; }
     }
     if (q0 + QB - 1 < kw0) continue;  // every query precedes this wave's keys
-    // S = Q K^T and dP = dO V^T : rows = queries, cols = keys (lane <-> key)
-    floatx16 sacc, dpacc;
-    zero16(sacc);
-    zero16(dpacc);
 #pragma unroll
-    for (int kk = 0; kk < D / 16; kk++) {
-      const int off = (lane & 31) * RP + kk * 16 + (lane >> 5) * 8;
-      sacc = mfma16(as_bf16x8(*reinterpret_cast<const uint4*>(sQ + off)), kf[kk], sacc);
-      dpacc = mfma16(as_bf16x8(*reinterpret_cast<const uint4*>(sdO + off)), vf[kk], dpacc);
-    }
+    for (int jb = 0; jb < NQ; jb++) {
+      if (q0 + jb * 32 + 31 < kw0) continue;  // this 32-query block precedes the wave's keys
+      // S = Q K^T and dP = dO V^T : rows = queries, cols = keys (lane <-> key)
+      floatx16 sacc, dpacc;
+      zero16(sacc);
+      zero16(dpacc);
 #pragma unroll
-    for (int e = 0; e < 16; e++) {
-      const int r = acc_row(e, lane);
-      const int qi = q0 + r;
-      float p = qi >= kj ? exp2f(sacc[e] * sl2 - sL[r]) : 0.f;
-      sacc[e] = p;
-      dpacc[e] = p * (dpacc[e] - sDi[r]);  // dS
-    }
-    // dV += P^T dO ; dK += dS^T Q   (A from registers: lane row = key, k-slice = its 8+8 queries)
+      for (int kk = 0; kk < D / 16; kk++) {
+        const int off = (jb * 32 + (lane & 31)) * RP + kk * 16 + (lane >> 5) * 8;
+        sacc = mfma16(as_bf16x8(*reinterpret_cast<const uint4*>(sQ + off)), kf[kk], sacc);
+        dpacc = mfma16(as_bf16x8(*reinterpret_cast<const uint4*>(sdO + off)), vf[kk], dpacc);
+      }
 #pragma unroll
-    for (int c = 0; c < 2; c++) {
-      const bf16x8 pf = pack8(sacc, 8 * c);
-      const bf16x8 sf = pack8(dpacc, 8 * c);
+      for (int e = 0; e < 16; e++) {
+        const int r = jb * 32 + acc_row(e, lane);
+        const int qi = q0 + r;
+        float p = qi >= kj ? exp2f(sacc[e] * sl2 - sL[r]) : 0.f;
+        sacc[e] = p;
+        dpacc[e] = p * (dpacc[e] - sDi[r]);  // dS
+      }
+      // dV += P^T dO ; dK += dS^T Q   (A from registers: lane row = key, k-slice = its 8+8 queries)
 #pragma unroll
-      for (int i = 0; i < D / 32; i++) {
-        dv[i] = mfma16(pf, tload(sdOt + (i * 32 + (lane & 31)) * TP, c * 16, lane), dv[i]);
-        dk[i] = mfma16(sf, tload(sQt + (i * 32 + (lane & 31)) * TP, c * 16, lane), dk[i]);
+      for (int c = 0; c < 2; c++) {
+        const bf16x8 pf = pack8(sacc, 8 * c);
+        const bf16x8 sf = pack8(dpacc, 8 * c);
+#pragma unroll
+        for (int i = 0; i < D / 32; i++) {
+          dv[i] = mfma16(pf, tload(sdOt + (i * 32 + (lane & 31)) * TP, jb * 32 + c * 16, lane), dv[i]);
+          dk[i] = mfma16(sf, tload(sQt + (i * 32 + (lane & 31)) * TP, jb * 32 + c * 16, lane), dk[i]);
+        }
       }
     }
   }
