@@ -24,6 +24,10 @@ namespace smhip {
 
 static constexpr float kLog2e = 1.4426950408889634f;
 
+// 2^x by the hardware v_exp_f32 (no denormal range handling: softmax weights below 2^-126
+// flush to zero, which is below the bf16 resolution of the products they feed)
+__device__ inline float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ inline floatx16 mfma16(const bf16x8& a, const bf16x8& b, const floatx16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
@@ -56,7 +60,7 @@ __device__ inline bf16x8 tload(const uint16_t* row, int c16, int lane) {
 template <int D, int NR, bool ROWS, bool TRANS>
 __device__ inline void stage(const uint16_t* __restrict__ g, int64_t ld, int r0, uint16_t* sRow,
                              uint16_t* sT) {
-  constexpr int RP = D + 8, TP = NR + 8;
+  constexpr int RP = D + 8, TP = NR + 4;
   if constexpr (ROWS) {
     for (int c = threadIdx.x; c < NR * D / 8; c += 256) {
       const int r = c / (D / 8), dc = (c % (D / 8)) * 8;
@@ -85,42 +89,47 @@ __device__ inline void stage(const uint16_t* __restrict__ g, int64_t ld, int r0,
 // global latency behind the compute.
 template <int D, int NR>
 struct Pref {
-  static constexpr int U = (NR / 2) * (D / 8);          // (row pair, chunk) units
+  static constexpr int U = (NR / 2) * (D / 8);  // (row pair, chunk) units
   static constexpr int PER = (U + 255) / 256;
-  uint4 a[PER], b[PER];
+  static_assert(PER <= 2, "Pref holds at most two units per thread");
+  uint4 a0, b0, a1, b1;  // named registers: no dynamically indexed (scratch) arrays
+  // unit c's two rows; units past U (only when U is not a multiple of 256) read row pair 0
+  __device__ static inline uint4 ld1(const uint16_t* __restrict__ g, int64_t ld, int r0, int c, int odd) {
+    if constexpr (U % 256 != 0) c = c < U ? c : 0;
+    const int rp = c % (NR / 2), dc = (c / (NR / 2)) * 8;
+    return *reinterpret_cast<const uint4*>(g + (int64_t)(r0 + 2 * rp + odd) * ld + dc);
+  }
   __device__ inline void load(const uint16_t* __restrict__ g, int64_t ld, int r0) {
+    a0 = ld1(g, ld, r0, threadIdx.x, 0);
+    b0 = ld1(g, ld, r0, threadIdx.x, 1);
+    if constexpr (PER > 1) {
+      a1 = ld1(g, ld, r0, 256 + threadIdx.x, 0);
+      b1 = ld1(g, ld, r0, 256 + threadIdx.x, 1);
+    }
+  }
+  template <bool ROWS, bool TRANS>
+  __device__ inline void store1(uint16_t* sRow, uint16_t* sT, int c, const uint4& a, const uint4& b) const {
+    constexpr int RP = D + 8, TP = NR + 4;
+    if (c >= U) return;
+    const int rp = c % (NR / 2), dc = (c / (NR / 2)) * 8;
+    if constexpr (ROWS) {
+      *reinterpret_cast<uint4*>(sRow + (2 * rp) * RP + dc) = a;
+      *reinterpret_cast<uint4*>(sRow + (2 * rp + 1) * RP + dc) = b;
+    }
+    if constexpr (TRANS) {
+      const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const int c = i * 256 + threadIdx.x;
-      if (c < U) {
-        const int rp = c % (NR / 2), dc = (c / (NR / 2)) * 8;
-        a[i] = *reinterpret_cast<const uint4*>(g + (int64_t)(r0 + 2 * rp) * ld + dc);
-        b[i] = *reinterpret_cast<const uint4*>(g + (int64_t)(r0 + 2 * rp + 1) * ld + dc);
+      for (int j = 0; j < 8; j++) {
+        const uint32_t lo = (j & 1) ? (av[j >> 1] >> 16) : (av[j >> 1] & 0xFFFFu);
+        const uint32_t hi = (j & 1) ? (bv[j >> 1] >> 16) : (bv[j >> 1] & 0xFFFFu);
+        *reinterpret_cast<uint32_t*>(sT + (dc + j) * TP + 2 * rp) = lo | (hi << 16);
       }
     }
   }
   template <bool ROWS, bool TRANS>
   __device__ inline void store(uint16_t* sRow, uint16_t* sT) const {
-    constexpr int RP = D + 8, TP = NR + 8;
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const int c = i * 256 + threadIdx.x;
-      if (c >= U) continue;
-      const int rp = c % (NR / 2), dc = (c / (NR / 2)) * 8;
-      if constexpr (ROWS) {
-        *reinterpret_cast<uint4*>(sRow + (2 * rp) * RP + dc) = a[i];
-        *reinterpret_cast<uint4*>(sRow + (2 * rp + 1) * RP + dc) = b[i];
-      }
-      if constexpr (TRANS) {
-        const uint32_t av[4] = {a[i].x, a[i].y, a[i].z, a[i].w}, bv[4] = {b[i].x, b[i].y, b[i].z, b[i].w};
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const uint32_t lo = (j & 1) ? (av[j >> 1] >> 16) : (av[j >> 1] & 0xFFFFu);
-          const uint32_t hi = (j & 1) ? (bv[j >> 1] >> 16) : (bv[j >> 1] & 0xFFFFu);
-          *reinterpret_cast<uint32_t*>(sT + (dc + j) * TP + 2 * rp) = lo | (hi << 16);
-        }
-      }
-    }
+    store1<ROWS, TRANS>(sRow, sT, threadIdx.x, a0, b0);
+    if constexpr (PER > 1) store1<ROWS, TRANS>(sRow, sT, 256 + threadIdx.x, a1, b1);
   }
 };
 
@@ -132,7 +141,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const uint16_t* __restrict_
                                                      const uint16_t* __restrict__ v, uint16_t* __restrict__ o,
                                                      float* __restrict__ lse, int S, int Hq, int Hkv, int64_t ldq,
                                                      int64_t ldk, int64_t ldv, int64_t ldo, float sl2) {
-  constexpr int KB = 64, KP = D + 8, VP = KB + 8;
+  constexpr int KB = 64, KP = D + 8, VP = KB + 4;
   __shared__ __attribute__((aligned(16))) uint16_t sK[KB * KP];
   __shared__ __attribute__((aligned(16))) uint16_t sVt[D * VP];
   const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest causal rows first
@@ -183,13 +192,13 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const uint16_t* __restrict_
       }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float mnew = fmaxf(m, mx);
-    const float alpha = exp2f(m - mnew);
+    const float alpha = fexp2(m - mnew);
     float rs = 0.f;
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        float p = exp2f(sacc[j][e] - mnew);
+        float p = fexp2(sacc[j][e] - mnew);
         sacc[j][e] = p;
         rs += p;
       }
@@ -258,7 +267,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
     float* __restrict__ dKh, float* __restrict__ dVh, int S, int Hq, int Hkv, int64_t ldq, int64_t ldk,
     int64_t ldv, int64_t lddo, float sl2, float scale) {
-  constexpr int QB = 64, NQ = QB / 32, RP = D + 8, TP = QB + 8;
+  constexpr int QB = 64, NQ = QB / 32, RP = D + 8, TP = QB + 4;
   __shared__ __attribute__((aligned(16))) uint16_t sQ[QB * RP];
   __shared__ __attribute__((aligned(16))) uint16_t sQt[D * TP];
   __shared__ __attribute__((aligned(16))) uint16_t sdO[QB * RP];
@@ -323,7 +332,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
       for (int e = 0; e < 16; e++) {
         const int r = jb * 32 + acc_row(e, lane);
         const int qi = q0 + r;
-        float p = qi >= kj ? exp2f(sacc[e] * sl2 - sL[r]) : 0.f;
+        float p = qi >= kj ? fexp2(sacc[e] * sl2 - sL[r]) : 0.f;
         sacc[e] = p;
         dpacc[e] = p * (dpacc[e] - sDi[r]);  // dS
       }
@@ -361,7 +370,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
     float* __restrict__ dq, int S, int Hq, int Hkv, int64_t ldq, int64_t ldk, int64_t ldv, int64_t lddo,
     int64_t lddq, float sl2, float scale) {
-  constexpr int KB = 64, RP = D + 8, TP = KB + 8;
+  constexpr int KB = 64, RP = D + 8, TP = KB + 4;
   __shared__ __attribute__((aligned(16))) uint16_t sK[KB * RP];
   __shared__ __attribute__((aligned(16))) uint16_t sKt[D * TP];
   __shared__ __attribute__((aligned(16))) uint16_t sV[KB * RP];
@@ -419,7 +428,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
 #pragma unroll
       for (int e = 0; e < 16; e++) {
         const int key = k0 + j * 32 + acc_row(e, lane);
-        float p = key <= qi ? exp2f(s[j][e] * sl2 - lq) : 0.f;
+        float p = key <= qi ? fexp2(s[j][e] * sl2 - lq) : 0.f;
         s[j][e] = p * (dp[j][e] - dq_i);  // dS^T
       }
     // dQ^T += K^T dS^T : A = K^T (lane row = d), B = dS^T from registers (lane col = query)
