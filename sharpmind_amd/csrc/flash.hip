@@ -272,7 +272,8 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t sQt[D * TP];
   __shared__ __attribute__((aligned(16))) uint16_t sdO[QB * RP];
   __shared__ __attribute__((aligned(16))) uint16_t sdOt[D * TP];
-  __shared__ float sL[QB], sDi[QB];
+  __shared__ __attribute__((aligned(16))) float sL[QB];
+  __shared__ __attribute__((aligned(16))) float sDi[QB];
   const int kbk = blockIdx.x;  // key block of 128
   const int h = blockIdx.y, b = blockIdx.z, kvh = h / (Hq / Hkv);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -328,13 +329,22 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
         sacc = mfma16(as_bf16x8(*reinterpret_cast<const uint4*>(sQ + off)), kf[kk], sacc);
         dpacc = mfma16(as_bf16x8(*reinterpret_cast<const uint4*>(sdO + off)), vf[kk], dpacc);
       }
+      // this lane's 16 rows are 4 runs of 4 consecutive queries: row statistics as float4
+      const bool diag = q0 + jb * 32 < kw0 + 31;  // some query of the block precedes some key
 #pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const int r = jb * 32 + acc_row(e, lane);
-        const int qi = q0 + r;
-        float p = qi >= kj ? fexp2(sacc[e] * sl2 - sL[r]) : 0.f;
-        sacc[e] = p;
-        dpacc[e] = p * (dpacc[e] - sDi[r]);  // dS
+      for (int g4 = 0; g4 < 4; g4++) {
+        const int r0 = jb * 32 + g4 * 8 + (lane >> 5) * 4;
+        const float4 L4 = *reinterpret_cast<const float4*>(sL + r0);
+        const float4 D4 = *reinterpret_cast<const float4*>(sDi + r0);
+        const float Lv[4] = {L4.x, L4.y, L4.z, L4.w}, Dv[4] = {D4.x, D4.y, D4.z, D4.w};
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const int e = g4 * 4 + u;
+          float p = fexp2(sacc[e] * sl2 - Lv[u]);
+          if (diag && q0 + r0 + u < kj) p = 0.f;
+          sacc[e] = p;
+          dpacc[e] = p * (dpacc[e] - Dv[u]);  // dS
+        }
       }
       // dV += P^T dO ; dK += dS^T Q   (A from registers: lane row = key, k-slice = its 8+8 queries)
 #pragma unroll
@@ -423,12 +433,13 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
         dp[j] = mfma16(as_bf16x8(*reinterpret_cast<const uint4*>(sV + off)), of[kk], dp[j]);
       }
     }
+    const bool diag = k0 + KB - 1 > qb * 128 + w * 32;  // some key of the tile follows some query
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        const int key = k0 + j * 32 + acc_row(e, lane);
-        float p = key <= qi ? fexp2(s[j][e] * sl2 - lq) : 0.f;
+        float p = fexp2(s[j][e] * sl2 - lq);
+        if (diag && k0 + j * 32 + acc_row(e, lane) > qi) p = 0.f;
         s[j][e] = p * (dp[j][e] - dq_i);  // dS^T
       }
     // dQ^T += K^T dS^T : A = K^T (lane row = d), B = dS^T from registers (lane col = query)
