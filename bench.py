@@ -41,15 +41,30 @@ def make_config(name):
     raise SystemExit(f"unknown config {name}")
 
 
+def gemm_dx_traffic():
+    """HBM bytes per launch of the backward dX GEMMs, measured offline with rocprofv3 --pmc
+    (FETCH_SIZE and WRITE_SIZE runs, scaled by a device-copy calibration); the summary with
+    the commands is profiles/gemm_dx_traffic_lora_q8_qwen3_0.6b_4x1024.md.  None if absent."""
+    path = os.path.join(ROOT, "profiles", "gemm_dx_traffic_lora_q8_qwen3_0.6b_4x1024.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(cfg, budget_s=30.0):
     """Time the oracle (scalar C restatement of BackpropEngine, one thread) on a bounded sample:
-    the same layer widths, vocab and adapters, one sequence of 16 tokens, with 1 and 2 layers;
+    the same layer widths, vocab and adapters, one sequence of 32 tokens, with 1 and 2 layers;
     the per-layer cost is the difference, extrapolated to cfg.n_layers (block fwd+bwd x L + head/CE)."""
     import numpy as np
     import oracle
     from sharpmind_amd.model import ModelConfig, tensor_specs
 
-    S = 16
+    S = 32
     rng = np.random.default_rng(0)
     times = {}
     for L in (1, 2):
@@ -59,7 +74,7 @@ def cpu_baseline(cfg, budget_s=30.0):
             if kind == "norm":
                 P[name] = np.ones(shape, np.float32)
             else:
-                P[name] = (rng.standard_normal(shape) * 0.02).astype(np.float32)
+                P[name] = rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)
             if (kind == "lora") if c.lora_rank else True:
                 G[name] = np.zeros(shape, np.float32)
         oc = oracle.EngineCfg(L=L, d=c.d_model, Hq=c.n_heads, Hkv=c.n_kv_heads, D=c.head_dim, F=c.ffn_dim,
@@ -77,7 +92,7 @@ def cpu_baseline(cfg, budget_s=30.0):
     return {"value": S / t_full, "unit": "tokens/s", "cores": 1, "kind": "port",
             "sample": f"oracle/engine.c scalar step (fwd+bwd), 1x{S} tokens, real widths/vocab/adapters, "
                       f"timed at 1 and 2 layers ({times[1]:.1f}s, {times[2]:.1f}s), extrapolated to "
-                      f"{cfg.n_layers} layers; S={S} underweights the attention S^2 term"}
+                      f"{cfg.n_layers} layers; S={S} underweights the attention S^2 term (about 15-20 s of CPU work)"}
 
 
 def main():
@@ -88,7 +103,19 @@ def main():
     ap.add_argument("--config", default="lora_q8")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one instead of replaying a graph")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 64 MiB device copy (byte reference for the HBM traffic counters)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        # reference for the rocprofv3 FETCH_SIZE / WRITE_SIZE counters: a device copy of 64 MiB
+        import torch
+        src = torch.empty(64 << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "device copy", "bytes_read": 64 << 20, "bytes_written": 64 << 20}))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported in this build "
               "(the data-parallel design is described in DESIGN.md; no multi-GPU figure is produced)",
@@ -131,23 +158,35 @@ def main():
     check(L.smhip_profile_begin(200000))
     for _ in range(psteps):
         eng.step(ids, labels, loss)
-    prof = (ctypes.c_double * 9)()
-    check(L.smhip_profile_end(prof, 3))
+    prof = (ctypes.c_double * 12)()
+    check(L.smhip_profile_end(prof, 4))
 
     ms_per_step = dt * 1e3 / args.steps
     tokens_per_s = T / (dt / args.steps)
-    gemm_ms, gemm_n, gemm_flops = prof[0], prof[1], prof[2]
     peak = PEAK_BF16_TFLOPS if cfg.precision == PREC_BF16 else PEAK_FP32_TFLOPS
-    achieved = (gemm_flops / gemm_n) / (gemm_ms / gemm_n * 1e-3) / 1e12 if gemm_n else 0.0
-    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(achieved / peak, 4), "traffic": None,
-                "kernel": "gemm_kernel (all linears, fwd+bwd)",
-                "launches_per_step": gemm_n / psteps, "avg_launch_us": round(gemm_ms / gemm_n * 1e3, 2) if gemm_n else None,
-                "gemm_ms_per_step": round(gemm_ms / psteps, 3),
+    cat = lambda c: (prof[3 * c], prof[3 * c + 1], prof[3 * c + 2])  # (ms, launches, flops)
+    g_ms, g_n, g_fl = cat(0)
+    dx_ms, dx_n, dx_fl = cat(3)
+    all_ms, all_n, all_fl = g_ms + dx_ms, g_n + dx_n, g_fl + dx_fl
+    tf = lambda fl, ms: round(fl / (ms * 1e-3) / 1e12, 2) if ms else None
+    if dx_n:  # dominant kernel: the backward dX GEMMs through the frozen quantised base
+        k_ms, k_n, k_fl = dx_ms, dx_n, dx_fl
+        kname = "gemm_kernel, B = quantised base column planes (backward dX = dY W, bf16 MFMA)"
+    else:
+        k_ms, k_n, k_fl = all_ms, all_n, all_fl
+        kname = "gemm_kernel (all linears, fwd+bwd)"
+    achieved = tf(k_fl, k_ms) or 0.0
+    roofline = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
+                "frac": round(achieved / peak, 4), "traffic": gemm_dx_traffic() if dx_n else None,
+                "kernel": kname,
+                "launches_per_step": k_n / psteps, "avg_launch_us": round(k_ms / k_n * 1e3, 2) if k_n else None,
+                "algorithmic_flops_per_launch": round(k_fl / k_n) if k_n else None,
+                "all_gemm": {"ms_per_step": round(all_ms / psteps, 3), "launches_per_step": all_n / psteps,
+                             "tflops": tf(all_fl, all_ms)},
                 "flash_fwd_ms_per_step": round(prof[3] / psteps, 3),
-                "flash_fwd_tflops": round(prof[5] / (prof[3] * 1e-3) / 1e12, 2) if prof[3] else None,
+                "flash_fwd_tflops": tf(prof[5], prof[3]),
                 "flash_bwd_ms_per_step": round(prof[6] / psteps, 3),
-                "flash_bwd_tflops": round(prof[8] / (prof[6] * 1e-3) / 1e12, 2) if prof[6] else None}
+                "flash_bwd_tflops": tf(prof[8], prof[6])}
     out = {
         "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3),

@@ -228,7 +228,8 @@ int smhip_engine_read_activation(void* engine, const char* what, int layer, void
 /* Live kernel timing on the calling thread: between begin and end, the GEMM and flash-attention
  * launchers bracket their kernels with HIP events on the launch stream.  end synchronises and writes
  * out[3*c + {0,1,2}] = (milliseconds, launches, algorithmic flops) for category c
- * (0 = MFMA GEMM kernel, 1 = flash forward, 2 = flash backward kernels), c < ncat. */
+ * (0 = MFMA GEMM kernel, 1 = flash forward, 2 = flash backward kernels, 3 = MFMA GEMM kernel with a
+ * quantised column-plane B operand, i.e. the backward dX products through the frozen base), c < ncat. */
 int smhip_profile_begin(int max_events);
 int smhip_profile_end(double* out, int ncat);
 /* Uniform random token ids in [0, vocab) (synthetic batches). */

@@ -168,7 +168,9 @@ int gemm(const GemmArgs& g, hipStream_t s);
 // ---------------------------------------------------------------- live kernel timing
 // When enabled (smhip_profile_begin) the launchers bracket their main kernel with
 // HIP events on the launch stream; smhip_profile_end sums the elapsed times.
-enum ProfCat { PROF_GEMM = 0, PROF_FLASH_FWD = 1, PROF_FLASH_BWD = 2, PROF_NCAT = 3 };
+// PROF_GEMM_DX: GEMMs whose B operand is a quantised base as column planes, i.e. the dX
+// products of the backward through the frozen weights (counted apart from PROF_GEMM)
+enum ProfCat { PROF_GEMM = 0, PROF_FLASH_FWD = 1, PROF_FLASH_BWD = 2, PROF_GEMM_DX = 3, PROF_NCAT = 4 };
 int prof_mark(hipStream_t s);                         // -1 when profiling is off
 bool profiling_active();
 void prof_add(int cat, int i0, int i1, double flops, int M = 0, int N = 0, int K = 0);

@@ -739,7 +739,8 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   const int ev0 = prof_mark(s);
   if (!dispatch(tile, a, am, bm, g.c_bf16, sp, s)) return 0;
   SMHIP_CHECK_LAUNCH();
-  prof_add(PROF_GEMM, ev0, prof_mark(s), 2.0 * g.M * g.N * ((double)g.K + g.K2), g.M, g.N, g.K + g.K2);
+  prof_add(bm == SRC_Q8T || bm == SRC_Q4KT ? PROF_GEMM_DX : PROF_GEMM, ev0, prof_mark(s),
+           2.0 * g.M * g.N * ((double)g.K + g.K2), g.M, g.N, g.K + g.K2);
   if (sp > 1) {
     const bool v4 = g.N % 4 == 0 && g.ldc % 4 == 0 && (!g.R || g.ldr % 4 == 0) && aligned_16(g.C) &&
                     (!g.R || aligned_16(g.R));
