@@ -41,6 +41,66 @@ def make_config(name):
     raise SystemExit(f"unknown config {name}")
 
 
+def elementwise_hbm(L, dev, reps=20):
+    """Config 2: the fused elementwise backward kernels at the configured shapes, timed with
+    events on the launch stream.  GB/s = algorithmic bytes (each input read once, each output
+    written once) / kernel time; frac against the 8 TB/s HBM peak."""
+    import torch
+    from sharpmind_amd import check
+    s = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    out = {}
+
+    def timed(name, fn, nbytes):
+        for _ in range(3):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        sec = e0.elapsed_time(e1) / reps * 1e-3
+        out[name] = {"us": round(sec * 1e6, 1), "bytes": nbytes, "gbs": round(nbytes / sec / 1e9, 1),
+                     "frac": round(nbytes / sec / 1e9 / PEAK_HBM_GBS, 4)}
+
+    T, D = 8192, 1024  # RMSNorm backward: dY, x_hat read; dX written (gamma / rmsInv are 40 KB)
+    dy = torch.randn(T, D, device=dev, generator=g)
+    xn = torch.randn(T, D, device=dev, generator=g)
+    rinv = torch.rand(T, device=dev, generator=g) + 0.5
+    gam = 1 + 0.1 * torch.randn(D, device=dev, generator=g)
+    dgam = torch.zeros(D, device=dev)
+    dx = torch.empty_like(dy)
+    timed("rmsnorm_bwd_8192x1024", lambda: check(L.smhip_grad_rmsnorm(dy.data_ptr(), xn.data_ptr(), rinv.data_ptr(),
+          gam.data_ptr(), dgam.data_ptr(), dx.data_ptr(), T, D, s)), 3 * T * D * 4)
+    del dy, xn, dx
+    T, F = 8192, 3072  # SwiGLU backward: dAct, gate, up read; [dg | du] written
+    da = torch.randn(T, F, device=dev, generator=g)
+    ga = torch.randn(T, F, device=dev, generator=g)
+    up = torch.randn(T, F, device=dev, generator=g)
+    dgu = torch.empty(T, 2 * F, device=dev)
+    timed("swiglu_bwd_8192x3072", lambda: check(L.smhip_grad_swiglu(da.data_ptr(), ga.data_ptr(), up.data_ptr(),
+          dgu.data_ptr(), T, F, s)), 5 * T * F * 4)
+    del da, ga, up, dgu
+    T, V = 8192, 32000  # cross-entropy backward: logits read once, dLogits written once
+    z = 2 * torch.randn(T, V, device=dev, generator=g)
+    lab = torch.randint(0, V, (T,), device=dev, dtype=torch.int32, generator=g)
+    dz = torch.empty_like(z)
+    loss = torch.zeros(1, device=dev)
+    timed("ce_bwd_8192x32000", lambda: check(L.smhip_ce_softmax_grad(z.data_ptr(), lab.data_ptr(), dz.data_ptr(),
+          loss.data_ptr(), T, V, -100, 0.0, s)), 2 * T * V * 4)
+    del z, dz
+    n = 100_000_000  # AdamW: param, grad, m, v read; param, m, v written
+    p = 0.02 * torch.randn(n, device=dev, generator=g)
+    gr = 0.02 * torch.randn(n, device=dev, generator=g)
+    m = 0.02 * torch.randn(n, device=dev, generator=g)
+    v = (0.02 * torch.randn(n, device=dev, generator=g)).abs_()
+    timed("adamw_100M", lambda: check(L.smhip_adamw_update(p.data_ptr(), gr.data_ptr(), m.data_ptr(), v.data_ptr(), n,
+          0.9, 0.95, 0.1, 0.05, 1e-4, 1e-8, 0.1, s)), 7 * n * 4)
+    return out
+
+
 def gemm_dx_traffic():
     """HBM bytes per launch of the backward dX GEMMs, measured offline with rocprofv3 --pmc
     (FETCH_SIZE and WRITE_SIZE runs, scaled by a device-copy calibration); the summary with
@@ -200,6 +260,8 @@ def main():
         "roofline": roofline,
     }
     del eng
+    torch.cuda.empty_cache()
+    out["elementwise_hbm"] = elementwise_hbm(L, dev)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg)
     print(json.dumps(out), flush=True)

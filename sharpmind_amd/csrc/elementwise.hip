@@ -15,6 +15,16 @@ static constexpr int kBlock = 256;
 
 __device__ inline float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 __device__ inline void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+// streaming (non-temporal) 16-byte accesses for data touched once per kernel
+typedef float f4v __attribute__((ext_vector_type(4)));
+__device__ inline float4 ldnt4(const float* p) {
+  const f4v v = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ inline void stnt4(float* p, float4 v) {
+  const f4v w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<f4v*>(p));
+}
 
 static int grid_for(int64_t work_items, int per_block, int max_blocks_per_cu = 8) {
   int64_t g = (work_items + per_block - 1) / per_block;
@@ -110,14 +120,34 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_bwd_kernel(
   }
 }
 
-// dst[d] += sum_g part[g*D + d], g ascending (deterministic).
-__global__ void column_reduce_add_kernel(const float* __restrict__ part, float* __restrict__ dst,
-                                         int G, int D) {
-  int d = blockIdx.x * blockDim.x + threadIdx.x;
-  if (d >= D) return;
+// dst[d] += sum_g part[g*D + d].  Block of 256 = 16 columns x 16 row groups; group j sums
+// rows g = j, j+16, ... (eight loads in flight), then the 16 group sums are added in
+// ascending j: a fixed order, so the result is deterministic.  grid = ceil(D / 16).
+__global__ __launch_bounds__(256) void column_reduce_add_kernel(const float* __restrict__ part,
+                                                                float* __restrict__ dst, int G, int D) {
+  __shared__ float sh[16][17];
+  const int c = threadIdx.x & 15, j = threadIdx.x >> 4;
+  const int d = blockIdx.x * 16 + c;
   float s = 0.f;
-  for (int g = 0; g < G; g++) s += part[(int64_t)g * D + d];
-  dst[d] += s;
+  if (d < D) {
+    for (int g0 = j; g0 < G; g0 += 16 * 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int g = g0 + 16 * u;
+        v[u] = g < G ? part[(int64_t)g * D + d] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) s += v[u];
+    }
+  }
+  sh[j][c] = s;
+  __syncthreads();
+  if (j == 0 && d < D) {
+    float t = 0.f;
+    for (int k = 0; k < 16; k++) t += sh[k][c];
+    dst[d] += t;
+  }
 }
 
 template <int VEC, int NCH, bool FROM_X, bool HAS_DW>
@@ -136,7 +166,7 @@ static int rmsnorm_bwd_launch(const float* dY, const float* x, const float* rinv
                      dY, x, rinv, w, dX, part, T, D, accumulate, dXb);
   SMHIP_CHECK_LAUNCH();
   if (HAS_DW) {
-    hipLaunchKernelGGL(column_reduce_add_kernel, dim3(ceil_div(D, 256)), dim3(256), 0, s, part, dw,
+    hipLaunchKernelGGL(column_reduce_add_kernel, dim3(ceil_div(D, 16)), dim3(256), 0, s, part, dw,
                        G, D);
     SMHIP_CHECK_LAUNCH();
   }
@@ -264,8 +294,8 @@ int layernorm_backward(const float* dY, const float* x, const float* w, float* d
   hipLaunchKernelGGL(layernorm_bwd_kernel, dim3(G), dim3(kBlock), 8 * D * sizeof(float), s, dY, x,
                      w, dX, part, part + (size_t)G * D, T, D, eps);
   SMHIP_CHECK_LAUNCH();
-  if (dw) hipLaunchKernelGGL(column_reduce_add_kernel, dim3(ceil_div(D, 256)), dim3(256), 0, s, part, dw, G, D);
-  if (db) hipLaunchKernelGGL(column_reduce_add_kernel, dim3(ceil_div(D, 256)), dim3(256), 0, s, part + (size_t)G * D, db, G, D);
+  if (dw) hipLaunchKernelGGL(column_reduce_add_kernel, dim3(ceil_div(D, 16)), dim3(256), 0, s, part, dw, G, D);
+  if (db) hipLaunchKernelGGL(column_reduce_add_kernel, dim3(ceil_div(D, 16)), dim3(256), 0, s, part + (size_t)G * D, db, G, D);
   SMHIP_CHECK_LAUNCH();
   return SMHIP_OK;
 }
@@ -309,7 +339,7 @@ __global__ __launch_bounds__(kBlock) void swiglu_bwd_v4_kernel(
   const int64_t n4 = (int64_t)T * F4;
   for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += (int64_t)gridDim.x * kBlock) {
     const int64_t t = i / F4, c = (i - t * F4) * 4;
-    float4 da = ld4(dA + t * F + c), g = ld4(G_ + t * F + c), u = ld4(U + t * F + c);
+    float4 da = ldnt4(dA + t * F + c), g = ldnt4(G_ + t * F + c), u = ldnt4(U + t * F + c);
     float ga[4] = {g.x, g.y, g.z, g.w}, ua[4] = {u.x, u.y, u.z, u.w}, daa[4] = {da.x, da.y, da.z, da.w};
     float og[4], ou[4];
 #pragma unroll
@@ -319,8 +349,8 @@ __global__ __launch_bounds__(kBlock) void swiglu_bwd_v4_kernel(
       og[v] = daa[v] * (sig * (1.f + ga[v] * (1.f - sig))) * ua[v];
     }
     float* row = out + t * 2 * (int64_t)F;
-    st4(row + c, make_float4(og[0], og[1], og[2], og[3]));
-    st4(row + F + c, make_float4(ou[0], ou[1], ou[2], ou[3]));
+    stnt4(row + c, make_float4(og[0], og[1], og[2], og[3]));
+    stnt4(row + F + c, make_float4(ou[0], ou[1], ou[2], ou[3]));
   }
 }
 
@@ -329,7 +359,7 @@ int swiglu_backward_f32(const float* dAct, const float* gate, const float* up, f
   if ((int64_t)T * F == 0) return SMHIP_OK;
   if (F % 4 == 0 && (uintptr_t)dAct % 16 == 0 && (uintptr_t)gate % 16 == 0 &&
       (uintptr_t)up % 16 == 0 && (uintptr_t)dFused % 16 == 0) {
-    hipLaunchKernelGGL(swiglu_bwd_v4_kernel, dim3(grid_for((int64_t)T * F / 4, kBlock)),
+    hipLaunchKernelGGL(swiglu_bwd_v4_kernel, dim3(grid_for((int64_t)T * F / 4, kBlock, 4)),
                        dim3(kBlock), 0, s, dAct, gate, up, dFused, T, F);
   } else {
     hipLaunchKernelGGL((swiglu_bwd_kernel<float, float>), dim3(grid_for((int64_t)T * F, kBlock)),
@@ -566,7 +596,7 @@ __global__ __launch_bounds__(NT) void ce_rows_reg_kernel(
     for (int j = 0; j < NV4; j++) {
       const int c = (j * NT + threadIdx.x) * 4;
       if (c + 3 < V) {
-        r[j] = ld4(z + c);
+        r[j] = ldnt4(z + c);
       } else {
         r[j].x = c < V ? z[c] : -INFINITY;
         r[j].y = c + 1 < V ? z[c + 1] : -INFINITY;
@@ -609,7 +639,7 @@ __global__ __launch_bounds__(NT) void ce_rows_reg_kernel(
       }
       if constexpr (sizeof(TOut) == 4) {
         if (c + 3 < V) {
-          st4((float*)(d + c), make_float4(e[0], e[1], e[2], e[3]));
+          stnt4((float*)(d + c), make_float4(e[0], e[1], e[2], e[3]));
         } else {
           for (int v = 0; v < 4; v++) if (c + v < V) d[c + v] = e[v];
         }
@@ -726,7 +756,7 @@ __global__ __launch_bounds__(NT) void ce_rows_2pass_vec_kernel(
     __syncthreads();  // z may alias d
     const float inv = 1.f / sum;
     for (int c4 = threadIdx.x; c4 < V4; c4 += NT) {
-      const float4 v = ld4(z + 4 * c4);
+      const float4 v = ldnt4(z + 4 * c4);
       float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int i = 0; i < 4; i++) {
@@ -741,7 +771,7 @@ __global__ __launch_bounds__(NT) void ce_rows_2pass_vec_kernel(
         e[i] = p * scale;
       }
       if constexpr (sizeof(TOut) == 4) {
-        st4((float*)(d + 4 * c4), make_float4(e[0], e[1], e[2], e[3]));
+        stnt4((float*)(d + 4 * c4), make_float4(e[0], e[1], e[2], e[3]));
       } else {
         *reinterpret_cast<uint2*>(d + 4 * c4) = make_uint2(pack_bf2(e[0], e[1]), pack_bf2(e[2], e[3]));
       }
@@ -829,14 +859,14 @@ __global__ __launch_bounds__(kBlock) void adamw_kernel(float* __restrict__ data,
   if (vec) {
     const int64_t n4 = n / 4;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += (int64_t)gridDim.x * kBlock) {
-      float4 d = ld4(data + 4 * i), g = ld4(grad + 4 * i), mm = ld4(m + 4 * i), vv = ld4(v + 4 * i);
+      float4 d = ldnt4(data + 4 * i), g = ldnt4(grad + 4 * i), mm = ldnt4(m + 4 * i), vv = ldnt4(v + 4 * i);
       adam_one(d.x, g.x, mm.x, vv.x, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
       adam_one(d.y, g.y, mm.y, vv.y, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
       adam_one(d.z, g.z, mm.z, vv.z, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
       adam_one(d.w, g.w, mm.w, vv.w, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
-      st4(m + 4 * i, mm);
-      st4(v + 4 * i, vv);
-      st4(data + 4 * i, d);
+      stnt4(m + 4 * i, mm);
+      stnt4(v + 4 * i, vv);
+      stnt4(data + 4 * i, d);
     }
     for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
       adam_one(data[i], grad[i], m[i], v[i], b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
