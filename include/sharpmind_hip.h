@@ -168,7 +168,7 @@ int smhip_flash_attention_backward(const void* q, const void* k, const void* v, 
 /* General dense GEMM on MFMA: C[M,N] = alpha * sum_k A(m,k) B(n,k) + beta * C.
  * Operand modes: 0 fp32 k-contiguous (X[r*ld + k]), 1 fp32 row-contiguous (X[k*ld + r]),
  * 2 bf16 k-contiguous, 3 bf16 row-contiguous.  C is fp32 (c_bf16 = 0) or bf16.  split_k > 1 splits
- * the reduction deterministically.  precision: SMHIP_PREC_FP32 (fp32 MFMA) or SMHIP_PREC_BF16. */
+ * the reduction deterministically; split_k = 0 lets the bf16 path choose tile and split.  precision: SMHIP_PREC_FP32 (fp32 MFMA) or SMHIP_PREC_BF16. */
 int smhip_gemm(int M, int N, int K, int a_mode, const void* A, int64_t lda, int b_mode, const void* B,
                int64_t ldb, float alpha, float beta, void* C, int64_t ldc, int c_bf16, int split_k,
                int precision, smhip_stream_t stream);

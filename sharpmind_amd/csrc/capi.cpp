@@ -575,7 +575,8 @@ int smhip_gemm(int M, int N, int K, int a_mode, const void* A, int64_t lda, int 
   g.alpha = alpha; g.beta = beta;
   g.C = C; g.ldc = ldc; g.c_bf16 = c_bf16;
   g.precision = precision;
-  g.split_k = split_k > 0 ? split_k : 1;
+  // split_k 0: the bf16 path picks the tile, ring depth and split itself (the engine's choice)
+  g.split_k = split_k > 0 ? split_k : (precision == SMHIP_PREC_BF16 ? 0 : 1);
   return gemm(g, STREAM(stream));
 }
 

@@ -162,14 +162,15 @@ struct GemmArgs {
   const float* bias;   // optional per-column bias added in the epilogue
   const float* R;      // optional residual: C = alpha*AB + bias + R  (fp32 output only)
   int64_t ldr;
+  int prof_cat;        // live-timing category (0: by operand kind)
 };
 int gemm(const GemmArgs& g, hipStream_t s);
 
 // ---------------------------------------------------------------- live kernel timing
 // When enabled (smhip_profile_begin) the launchers bracket their main kernel with
 // HIP events on the launch stream; smhip_profile_end sums the elapsed times.
-// PROF_GEMM_DX: GEMMs whose B operand is a quantised base as column planes, i.e. the dX
-// products of the backward through the frozen weights (counted apart from PROF_GEMM)
+// PROF_GEMM_DX: the dX products of the backward through the frozen base weights (B a
+// quantised base as column planes, or tagged by the caller), counted apart from PROF_GEMM
 enum ProfCat { PROF_GEMM = 0, PROF_FLASH_FWD = 1, PROF_FLASH_BWD = 2, PROF_GEMM_DX = 3, PROF_NCAT = 4 };
 int prof_mark(hipStream_t s);                         // -1 when profiling is off
 bool profiling_active();

@@ -44,6 +44,8 @@ struct LayerW {
   void* qraw[4] = {};        // LoRA mode: planes storage
   QuantPlanes qt[4];         // LoRA bf16 mode: column planes (transposed copy) for dX
   void* qtraw[4] = {};
+  uint16_t* wb[4] = {};      // LoRA bf16 mode with the base workspace: bf16 [Out][In] and [In][Out]
+  uint16_t* wbt[4] = {};
   DenseRef la[4], lb[4];     // LoRA A [In, nr], B [nr, Out]
   int* lb_cols = nullptr;    // device: column start of each diagonal block
 };
@@ -69,6 +71,11 @@ struct Engine {
   // tensors
   DenseRef emb, norm_f;
   QuantPlanes emb_q{}, emb_qt{};
+  // bf16 LoRA engines decode the frozen quantised base once per step into bf16 copies in both
+  // layouts (row for y = x W^T, transposed for dX = dY W), so every base GEMM streams bf16
+  // straight to LDS; without room for it the GEMMs decode the codes in their loaders
+  bool base_ws = false;
+  uint16_t *emb_b = nullptr, *emb_bt = nullptr;
   std::vector<LayerW> L;
   std::map<std::string, DenseRef*> dense_by_name;
   // activations
@@ -197,7 +204,31 @@ static int build(Engine* e) {
     for (int l = 0; l < c.n_layers; l++)
       for (int p = 0; p < 4; p++)
         if (int rc = mk(&e->L[l].q[p], &e->L[l].qraw[p], (int64_t)e->Out[p] * e->In[p])) return rc;
-    if (e->bf) {  // column planes for the bf16 dX GEMMs
+    if (e->bf) {  // bf16 base workspace when dims allow and it takes at most a quarter of free HBM
+      int64_t n_all = (int64_t)V * d;
+      bool dims_ok = d % 16 == 0 && V % 16 == 0;
+      for (int p = 0; p < 4; p++) {
+        n_all += (int64_t)c.n_layers * e->Out[p] * e->In[p];
+        dims_ok = dims_ok && e->Out[p] % 16 == 0 && e->In[p] % 16 == 0;
+      }
+      size_t fr = 0, tot = 0;
+      if (hipMemGetInfo(&fr, &tot) != hipSuccess) fr = 0;
+      const char* ev = getenv("SMHIP_BASE_WS");  // SMHIP_BASE_WS=0 keeps the fused-decode GEMMs
+      e->base_ws = dims_ok && (size_t)n_all * 4 <= fr / 4 && !(ev && atoi(ev) == 0);
+    }
+    if (e->base_ws) {
+      auto bfbuf = [&](uint16_t** dst, int64_t n) -> int {
+        *dst = (uint16_t*)dalloc(e, 2 * (size_t)n);
+        return *dst ? SMHIP_OK : fail(SMHIP_ENOMEM, "engine: bf16 base workspace");
+      };
+      if (int rc = bfbuf(&e->emb_b, (int64_t)V * d)) return rc;
+      if (int rc = bfbuf(&e->emb_bt, (int64_t)V * d)) return rc;
+      for (int l = 0; l < c.n_layers; l++)
+        for (int p = 0; p < 4; p++) {
+          if (int rc = bfbuf(&e->L[l].wb[p], (int64_t)e->Out[p] * e->In[p])) return rc;
+          if (int rc = bfbuf(&e->L[l].wbt[p], (int64_t)e->Out[p] * e->In[p])) return rc;
+        }
+    } else if (e->bf) {  // column planes for the bf16 dX GEMMs
       void* emb_t = nullptr;
       if (int rc = mk(&e->emb_qt, &emb_t, (int64_t)V * d)) return rc;
       for (int l = 0; l < c.n_layers; l++)
@@ -305,6 +336,7 @@ static Operand act_r(const Engine* e, const void* p, int64_t ld) {
 }
 // weight W[Out][In] as the B operand of  y = x W^T (k = In contiguous)
 static Operand w_fwd(const Engine* e, const LayerW& w, int p) {
+  if (e->base_ws) return Operand{SRC_BF16_K, w.wb[p], nullptr, e->In[p]};
   if (e->lora) {
     const QuantPlanes& q = w.q[p];
     return Operand{q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8_K : SRC_Q4K_K, q.qs, q.sc, e->In[p]};
@@ -313,6 +345,7 @@ static Operand w_fwd(const Engine* e, const LayerW& w, int p) {
 }
 // weight as the B operand of  dX = dY W  (n = In, k = Out)
 static Operand w_bwd(const Engine* e, const LayerW& w, int p) {
+  if (e->base_ws) return Operand{SRC_BF16_K, w.wbt[p], nullptr, e->Out[p]};
   if (e->lora && e->bf) {
     const QuantPlanes& q = w.qt[p];
     return Operand{q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8T : SRC_Q4KT, q.qs, q.sc, e->Out[p]};
@@ -449,6 +482,7 @@ static int proj_backward(Engine* e, int l, int p, const void* dY, const float* d
   g.split_k = split_arg(e, T, In, Out);
   g.A = act_k(e, dY, Out);
   g.B = w_bwd(e, w, p);
+  if (e->lora) g.prof_cat = PROF_GEMM_DX;
   g.C = dX_out ? dX_out : (void*)dX; g.ldc = In; g.c_bf16 = dX_bf16;
   return gemm(g, s);
 }
@@ -460,6 +494,12 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
   int rc;
 #define R_(x) do { if ((rc = (x))) return rc; } while (0)
   R_(zero_bytes(e->grad, sizeof(float) * (size_t)e->n_train, s));  // optimizer.ZeroGrad (TrainLoop.cs:109)
+
+  if (e->base_ws) {  // decode the frozen base into the bf16 workspace (both layouts)
+    R_(dequant_bf16(e->emb_q, V, d, e->emb_b, e->emb_bt, s));
+    for (int l = 0; l < c.n_layers; l++)
+      for (int p = 0; p < 4; p++) R_(dequant_bf16(e->L[l].q[p], e->Out[p], e->In[p], e->L[l].wb[p], e->L[l].wbt[p], s));
+  }
 
   // ---------------- forward
   if (e->lora) {
@@ -500,7 +540,8 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
     g.precision = prec(e); g.alpha = 1.f; g.split_k = 1;
     g.M = T; g.N = V; g.K = d;
     g.A = act_k(e, e->xnf, d);
-    if (e->lora) g.B = Operand{e->emb_q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8_K : SRC_Q4K_K, e->emb_q.qs, e->emb_q.sc, d};
+    if (e->base_ws) g.B = Operand{SRC_BF16_K, e->emb_b, nullptr, d};
+    else if (e->lora) g.B = Operand{e->emb_q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8_K : SRC_Q4K_K, e->emb_q.qs, e->emb_q.sc, d};
     else g.B = e->emb.bf ? Operand{SRC_BF16_K, e->emb.bf, nullptr, d} : Operand{SRC_F32_K, e->emb.data, nullptr, d};
     g.C = e->logits; g.ldc = V;
     R_(gemm(g, s));
@@ -515,11 +556,13 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
     g.precision = prec(e); g.alpha = 1.f; g.split_k = 1;
     g.M = T; g.N = d; g.K = V;
     g.A = act_k(e, e->dlogits, V);
-    if (e->lora && e->bf) g.B = Operand{e->emb_qt.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8T : SRC_Q4KT, e->emb_qt.qs, e->emb_qt.sc, V};
+    if (e->base_ws) g.B = Operand{SRC_BF16_K, e->emb_bt, nullptr, V};
+    else if (e->lora && e->bf) g.B = Operand{e->emb_qt.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8T : SRC_Q4KT, e->emb_qt.qs, e->emb_qt.sc, V};
     else if (e->lora) g.B = Operand{e->emb_q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8_R : SRC_Q4K_R, e->emb_q.qs, e->emb_q.sc, d};
     else g.B = e->emb.bf ? Operand{SRC_BF16_R, e->emb.bf, nullptr, d} : Operand{SRC_F32_R, e->emb.data, nullptr, d};
     g.C = e->dx; g.ldc = d;
     g.split_k = split_arg(e, T, d, V);
+    if (e->lora) g.prof_cat = PROF_GEMM_DX;
     R_(gemm(g, s));
     if (!e->lora) {
       GemmArgs gw{};
@@ -659,7 +702,7 @@ int smhip_engine_param_count(void* engine, int64_t* trainable, int64_t* frozen) 
 
 // rebuild the column planes of row planes q (bf16 LoRA engines keep both)
 static int refresh_cols(Engine* e, const QuantPlanes* q, hipStream_t s) {
-  if (!e->bf || !e->lora) return SMHIP_OK;
+  if (!e->bf || !e->lora || e->base_ws) return SMHIP_OK;
   QuantPlanes out;
   if (q == &e->emb_q) return make_col_planes(*q, e->c.vocab, e->c.d_model, e->emb_qt.qs, &out, s);
   for (auto& w : e->L)

@@ -19,7 +19,14 @@
 // column beyond the matrix reads 0 (or, for row-contiguous operands, unrelated values that
 // only reach C rows/columns that are never stored), so the main loop has no guards.
 // Pipelining: the next K tile's loads (DMA or registers) are issued before the current
-// tile's MFMAs; double-buffered LDS, one barrier per K tile.
+// tile's MFMAs; double-buffered LDS, one barrier per K tile.  When both operands are direct
+// DMA and LDS allows, a ring of ST stages keeps ST-1 tiles in flight; its barrier carries no
+// memory fence (a fence would wait for every outstanding load and drain the ring), each
+// wave instead waits with vmcnt for the one stage it needs.  Products whose output has at
+// most one 128x128 tile per CU use an 8-wave 128x128 tile (two waves per SIMD, each 64 x 32)
+// with a 3-stage ring and no split.
+// Products with a side of at most 64 (the LoRA rank GEMMs) go to the streaming kernel of
+// skinny.hip.
 // Workgroups are numbered so that each of the 8 XCDs owns a contiguous band of output
 // tiles (consecutive workgroups are dispatched round-robin over XCDs), swept in groups of 8
 // m-panels so that operand panels are reused from that XCD's L2.
@@ -47,6 +54,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes)
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
 }
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+template <int N>
+__device__ __forceinline__ void wait_vm_n() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+// workgroup barrier without the memory fence of __syncthreads (which waits for every
+// outstanding load, i.e. drains the DMA ring); callers wait for the stage they need with
+// wait_vm_n, and LDS reads are complete because their MFMAs consumed them
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 // swizzled byte offset of 16-byte chunk c (0..7) of row r in a [rows][64] bf16 tile
 __device__ __forceinline__ int sw(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
@@ -344,24 +361,24 @@ struct Args {
   float* partial;   // non-null: write raw partial sums [split][M][N] instead of C
 };
 
-template <int BM, int BN, int WGM, int NW>
+template <int BM, int BN, int WGM, int NW, int ST = 2>
 struct Shape {
   static constexpr int NT = 64 * NW;
   static constexpr int WGN = NW / WGM;
   static constexpr int WM = BM / WGM, WN = BN / WGN;
   static constexpr int MB = WM / 32, NB = WN / 32;
-  static constexpr int LDS = 2 * (BM + BN) * 128;
+  static constexpr int LDS = ST * (BM + BN) * 128;
   static constexpr int OCC = LDS * 2 <= 160 * 1024 && MB * NB <= 8 && NW == 4 ? 2 : 1;
 };
 
-template <int BM, int BN, int WGM, int NW, int AMODE, int BMODE, bool C_BF16>
-__global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW>::OCC)) void gemm_kernel(Args g) {
-  using S = Shape<BM, BN, WGM, NW>;
+template <int BM, int BN, int WGM, int NW, int AMODE, int BMODE, bool C_BF16, int ST = 2>
+__global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW, ST>::OCC)) void gemm_kernel(Args g) {
+  using S = Shape<BM, BN, WGM, NW, ST>;
   constexpr int NT = S::NT;
   constexpr int MB = S::MB, NB = S::NB;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[S::LDS];
   auto sA = [&](int buf) -> uint8_t* { return smem + buf * (BM * 128); };
-  auto sB = [&](int buf) -> uint8_t* { return smem + 2 * BM * 128 + buf * (BN * 128); };
+  auto sB = [&](int buf) -> uint8_t* { return smem + ST * BM * 128 + buf * (BN * 128); };
 
   const int ntiles = g.tiles_m * g.tiles_n;
   const int wg = blockIdx.x;
@@ -398,7 +415,9 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW>::OCC)) void gemm_k
   const int nk2 = split == nsplit - 1 ? (g.K2 + BK - 1) / BK : 0;
 
   // fragments of k-slice kk+1 are read from LDS while the MFMAs of slice kk run
-  auto compute = [&](int buf) {
+  // mid() runs once the first fragments of the tile are requested (it issues the next
+  // tile's global loads, overlapping their issue with the LDS round trip)
+  auto compute = [&](int buf, auto&& mid) {
     const uint8_t* a = sA(buf);
     const uint8_t* b = sB(buf);
     bf16x8 fa[2][MB], fb[2][NB];
@@ -410,18 +429,49 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW>::OCC)) void gemm_k
       for (int j = 0; j < NB; j++) fb[p][j] = *reinterpret_cast<const bf16x8*>(b + sw(wn * S::WN + j * 32 + (lane & 31), ch));
     };
     rd(0, 0);
+    mid();
 #pragma unroll
     for (int kk = 0; kk < BK / 16; kk++) {
+      // the scheduling barriers keep the two fragment sets apart: without them the reads of
+      // slice kk+1 sink below the MFMAs of slice kk into the same registers and every
+      // slice waits out a full LDS round trip
       if (kk + 1 < BK / 16) rd(kk + 1, (kk + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);
       const int p = kk & 1;
 #pragma unroll
       for (int i = 0; i < MB; i++)
 #pragma unroll
         for (int j = 0; j < NB; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[p][i], fb[p][j], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  if (nk1 > 0) {
+  if constexpr (ST > 2) {
+    // ST-stage ring (direct-to-LDS operands only): tiles t+1 .. t+ST-2 are in flight while
+    // tile t is multiplied; the barrier at the top of iteration t also frees the stage of
+    // tile t-1, which is refilled with tile t+ST-1
+    static_assert(AMODE == SRC_BF16_K && BMODE == SRC_BF16_K, "the ring stages direct-to-LDS operands only");
+    constexpr int PER = decltype(la)::NI + decltype(lb)::NI;  // DMA instructions per wave per tile
+#pragma unroll
+    for (int t = 0; t < ST - 1; t++)
+      if (t < nk1) {
+        la.fetch(sA(t), (kt0 + t) * BK);
+        lb.fetch(sB(t), (kt0 + t) * BK);
+      }
+    for (int t = 0; t < nk1; t++) {
+      if (t + ST - 2 < nk1) wait_vm_n<(ST - 2) * PER>();
+      else wait_vm();
+      ring_barrier();
+      compute(t % ST, [&] {
+        if (t + ST - 1 < nk1) {
+          const int st = (t + ST - 1) % ST;
+          la.fetch(sA(st), (kt0 + t + ST - 1) * BK);
+          lb.fetch(sB(st), (kt0 + t + ST - 1) * BK);
+        }
+      });
+    }
+    if (nk2 > 0) __syncthreads();
+  } else if (nk1 > 0) {
     la.fetch(sA(0), kt0 * BK);
     lb.fetch(sB(0), kt0 * BK);
     la.commit(sA(0));
@@ -431,11 +481,12 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW>::OCC)) void gemm_k
     for (int t = 0; t < nk1; t++) {
       const int buf = t & 1;
       const bool more = t + 1 < nk1;
-      if (more) {
-        la.fetch(sA(buf ^ 1), (kt0 + t + 1) * BK);
-        lb.fetch(sB(buf ^ 1), (kt0 + t + 1) * BK);
-      }
-      compute(buf);
+      compute(buf, [&] {
+        if (more) {
+          la.fetch(sA(buf ^ 1), (kt0 + t + 1) * BK);
+          lb.fetch(sB(buf ^ 1), (kt0 + t + 1) * BK);
+        }
+      });
       if (more) {
         la.commit(sA(buf ^ 1));
         lb.commit(sB(buf ^ 1));
@@ -448,7 +499,7 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW>::OCC)) void gemm_k
     ext_tile<BM, NT>(g.amode2, g.ext_vec != 0, g.A2, m0, t * BK, g.M, g.K2, g.alpha2, sA(0));
     ext_tile<BN, NT>(g.bmode2, g.ext_vec != 0, g.B2, n0, t * BK, g.N, g.K2, 1.f, sB(0));
     __syncthreads();
-    compute(0);
+    compute(0, [] {});
     __syncthreads();
   }
 
@@ -561,7 +612,7 @@ __global__ void splitk_epilogue_kernel(const float* __restrict__ partial, int sp
 // 256x256 runs 8 waves (2 x 4, each 128 x 64); the others 4 waves.  64x128 and 128x64 are
 // for skinny products (LoRA rank on one side), which are bandwidth-bound: many small
 // workgroups plus split-K keep every CU streaming.
-enum TileId { T256x256 = 0, T256x128 = 1, T128x128 = 2, T256x64 = 3, T64x128 = 4, T128x64 = 5, NTILE = 6 };
+enum TileId { T256x256 = 0, T256x128 = 1, T128x128 = 2, T256x64 = 3, T64x128 = 4, T128x64 = 5, T128x128W8 = 6, NTILE = 7 };
 struct TileInfo { int bm, bn, occ; double eff; };
 // eff: relative MFMA throughput per CU of the tile shape (larger tiles re-read less LDS/L2)
 static const TileInfo kTiles[NTILE] = {
@@ -571,11 +622,32 @@ static const TileInfo kTiles[NTILE] = {
     {256, 64, Shape<256, 64, 4, 4>::OCC, 0.60},
     {64, 128, Shape<64, 128, 1, 4>::OCC, 0.50},
     {128, 64, Shape<128, 64, 4, 4>::OCC, 0.50},
+    {128, 128, Shape<128, 128, 2, 8>::OCC, 0.88},
 };
 
+// ring depth of the direct-to-LDS 128x128 kernels: 3 stages for the 8-wave tile (one
+// workgroup per CU, so LDS is free for a deeper ring), double buffering otherwise;
+// SMHIP_GEMM_STAGES=2..4 overrides (tuning runs)
+static int ring_stages(int nw) {
+  static const int v = [] { const char* e = getenv("SMHIP_GEMM_STAGES"); return e ? atoi(e) : 0; }();
+  return v ? v : (nw == 8 ? 3 : 2);
+}
 template <int BM, int BN, int WGM, int NW, int AM, int BMD>
 static void launch_c(const Args& a, int c_bf16, int splits, hipStream_t s) {
   const dim3 grid(a.tiles_m * a.tiles_n, splits);
+  if constexpr (AM == SRC_BF16_K && BMD == SRC_BF16_K && BM + BN <= 256) {
+    const int st = ring_stages(NW);
+    if (st == 3 || st == 4) {
+      if (c_bf16 && !a.partial) {
+        if (st == 3) hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, true, 3>), grid, dim3(64 * NW), 0, s, a);
+        else hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, true, 4>), grid, dim3(64 * NW), 0, s, a);
+      } else {
+        if (st == 3) hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, false, 3>), grid, dim3(64 * NW), 0, s, a);
+        else hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, false, 4>), grid, dim3(64 * NW), 0, s, a);
+      }
+      return;
+    }
+  }
   if (c_bf16 && !a.partial) hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, true>), grid, dim3(64 * NW), 0, s, a);
   else hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, false>), grid, dim3(64 * NW), 0, s, a);
 }
@@ -588,6 +660,7 @@ static void launch_tile(int tile, const Args& a, int c_bf16, int sp, hipStream_t
     case T128x128: launch_c<128, 128, 2, 4, AM, BMD>(a, c_bf16, sp, s); break;
     case T256x64: launch_c<256, 64, 4, 4, AM, BMD>(a, c_bf16, sp, s); break;
     case T64x128: launch_c<64, 128, 1, 4, AM, BMD>(a, c_bf16, sp, s); break;
+    case T128x128W8: launch_c<128, 128, 2, 8, AM, BMD>(a, c_bf16, sp, s); break;
     default: launch_c<128, 64, 4, 4, AM, BMD>(a, c_bf16, sp, s); break;
   }
 }
@@ -664,6 +737,15 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   const bool a_ok = am == SRC_BF16_K || am == SRC_BF16_R;
   const bool b_ok = bm == SRC_BF16_K || bm == SRC_BF16_R || bm == SRC_Q8_K || bm == SRC_Q8T || bm == SRC_Q4K_K || bm == SRC_Q4KT;
   if (!a_ok || !b_ok) return 0;
+  // a side of at most 64 (the LoRA rank products): the bandwidth-bound skinny kernel
+  if (g.K2 == 0 && !g.bias && !g.R && (g.N <= 64 || g.M <= 64) && (bm == SRC_BF16_K || bm == SRC_BF16_R)) {
+    const int r = g.N <= 64
+        ? gemm_skinny(g.M, g.N, g.K, g.A.p, g.A.ld, am == SRC_BF16_K, g.B.p, g.B.ld, bm == SRC_BF16_K, g.alpha,
+                      g.beta, g.C, g.ldc, false, g.c_bf16 != 0, s)
+        : gemm_skinny(g.N, g.M, g.K, g.B.p, g.B.ld, bm == SRC_BF16_K, g.A.p, g.A.ld, am == SRC_BF16_K, g.alpha,
+                      g.beta, g.C, g.ldc, true, g.c_bf16 != 0, s);
+    if (r != 0) return r;
+  }
   if (am == SRC_BF16_R && bm != SRC_BF16_R) return 0;
   if (!aligned_16(g.A.p) || !aligned_16(g.B.p)) return 0;
   if (am == SRC_BF16_K && g.A.ld % 8) return 0;
@@ -714,10 +796,15 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
     // products), keep >= 8 (skinny: 2) K tiles per split and the partials under 64 MiB
     tile = pick_tile(g.M, g.N, 1, bm);
     const bool sk = skinny(g.M, g.N);
+    // at most one 128x128 tile per CU and a moderate K: the 8-wave tile (two waves per SIMD
+    // hide LDS and barrier latency) with a ring, whole K per workgroup, beats split-K
+    const bool w8 = tile == T128x128 && am == SRC_BF16_K && bm == SRC_BF16_K && !sk &&
+                    (int64_t)ceil_div(g.M, 128) * ceil_div(g.N, 128) <= num_cus() && nk < 96;
+    if (w8) tile = T128x128W8;
     const int64_t tiles = (int64_t)ceil_div(g.M, kTiles[tile].bm) * ceil_div(g.N, kTiles[tile].bn);
     const int64_t target = (int64_t)num_cus() * kTiles[tile].occ * (sk ? 2 : 1);
     sp = 1;
-    if (tiles < target) {
+    if (tiles < target && !w8) {
       sp = (int)std::min<int64_t>((target + tiles - 1) / tiles, nk / (sk ? 2 : 8));
       sp = std::max(1, std::min(sp, 64));
       while (sp > 1 && (int64_t)sp * g.M * g.N * 4 > ((int64_t)64 << 20)) sp--;
@@ -739,7 +826,7 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   const int ev0 = prof_mark(s);
   if (!dispatch(tile, a, am, bm, g.c_bf16, sp, s)) return 0;
   SMHIP_CHECK_LAUNCH();
-  prof_add(bm == SRC_Q8T || bm == SRC_Q4KT ? PROF_GEMM_DX : PROF_GEMM, ev0, prof_mark(s),
+  prof_add(g.prof_cat ? g.prof_cat : (bm == SRC_Q8T || bm == SRC_Q4KT ? PROF_GEMM_DX : PROF_GEMM), ev0, prof_mark(s),
            2.0 * g.M * g.N * ((double)g.K + g.K2), g.M, g.N, g.K + g.K2);
   if (sp > 1) {
     const bool v4 = g.N % 4 == 0 && g.ldc % 4 == 0 && (!g.R || g.ldr % 4 == 0) && aligned_16(g.C) &&

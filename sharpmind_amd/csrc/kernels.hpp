@@ -39,6 +39,9 @@ int colsum_add(const float* dY, float* db, int B, int Out, hipStream_t s);
 
 // gemm_bf16.hip: 1 = ran, 0 = not eligible (generic kernel), <0 = error
 int gemm_bf16_fast(const GemmArgs& g, hipStream_t s);
+int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, const void* small, int64_t lds,
+                bool small_k, float alpha, float beta, void* C, int64_t ldc, bool trans_out, bool c_bf16,
+                hipStream_t s);
 
 // quant.hip
 int dequant_raw(int qtype, const void* raw, float* out, int64_t n, hipStream_t s);
@@ -46,6 +49,7 @@ size_t planes_bytes(int qtype, int64_t n, size_t* qs_bytes);
 int repack_planes(int qtype, const void* raw, int64_t n, void* dst, QuantPlanes* out, hipStream_t s);
 int dequant_rows(const QuantPlanes& q, const int32_t* ids, float* out, int T, int D, hipStream_t s);
 int make_col_planes(const QuantPlanes& q, int rows, int cols, void* dst, QuantPlanes* out, hipStream_t s);
+int dequant_bf16(const QuantPlanes& q, int rows, int cols, uint16_t* w, uint16_t* wt, hipStream_t s);
 
 // attention.hip
 int attention_slot_backward(const float* dO, const float* q, const float* k, const float* v,

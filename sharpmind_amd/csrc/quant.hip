@@ -226,3 +226,74 @@ int dequant_rows(const QuantPlanes& q, const int32_t* ids, float* out, int T, in
   return SMHIP_OK;
 }
 }  // namespace smhip
+
+namespace smhip {
+// ---------------------------------------------------------------- bf16 workspace of a frozen base
+// Decodes a quantised [rows][cols] matrix to bf16 (the fp32 weight q*d, or sd*v - md, rounded
+// once, exactly the values the fused-decode GEMM loaders stage into LDS) in the row layout
+// w[o*cols + i] and/or the transposed layout wt[i*rows + o].  One workgroup per 64 x 64 tile:
+// each thread decodes 16 consecutive elements of one row (one 16-byte code load, one scale),
+// writes them to the row layout and to an LDS tile, from which 16 consecutive rows of one
+// column are written to the transposed layout.
+__global__ __launch_bounds__(256) void dequant_bf16_kernel(QuantPlanes q, int rows, int cols,
+                                                           uint16_t* __restrict__ w, uint16_t* __restrict__ wt) {
+  __shared__ uint16_t tile[64][64 + 2];
+  const int tr = threadIdx.x >> 2, tc = (threadIdx.x & 3) * 16;
+  const int o = blockIdx.y * 64 + tr, i0 = blockIdx.x * 64 + tc;
+  if (o < rows && i0 < cols) {
+    const int64_t e = (int64_t)o * cols + i0;
+    float v[16];
+    if (q.kind == SMHIP_QTYPE_Q8_0) {
+      const uint4 c = *reinterpret_cast<const uint4*>((const int8_t*)q.qs + e);
+      const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+      const float d = q.sc[e >> 5];
+#pragma unroll
+      for (int j = 0; j < 16; j++) v[j] = (float)(int8_t)(cw[j >> 2] >> ((j & 3) * 8)) * d;
+    } else {
+      const int wi = (int)(e & 255);
+      const uint4 c = *reinterpret_cast<const uint4*>((const uint8_t*)q.qs + (e >> 8) * 128 + (wi >> 6) * 32 + (wi & 31));
+      const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+      const int sh = ((wi & 63) >> 5) * 4;
+      const float sd = q.sc[2 * (e >> 5)], md = q.sc[2 * (e >> 5) + 1];
+#pragma unroll
+      for (int j = 0; j < 16; j++) v[j] = sd * (float)((cw[j >> 2] >> ((j & 3) * 8 + sh)) & 0xF) - md;
+    }
+    uint32_t p[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) p[j] = pack_bf2(v[2 * j], v[2 * j + 1]);
+    if (w) {
+      uint4* dst = reinterpret_cast<uint4*>(w + e);
+      dst[0] = make_uint4(p[0], p[1], p[2], p[3]);
+      dst[1] = make_uint4(p[4], p[5], p[6], p[7]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      tile[tr][tc + 2 * j] = (uint16_t)(p[j] & 0xFFFF);
+      tile[tr][tc + 2 * j + 1] = (uint16_t)(p[j] >> 16);
+    }
+  }
+  if (!wt) return;
+  __syncthreads();
+  // transposed: thread -> column i = i-tile + tr, rows o0 .. o0+15
+  const int i = blockIdx.x * 64 + tr, o0 = blockIdx.y * 64 + tc;
+  if (i < cols && o0 < rows) {
+    uint32_t p[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) p[j] = (uint32_t)tile[tc + 2 * j][tr] | ((uint32_t)tile[tc + 2 * j + 1][tr] << 16);
+    uint4* dst = reinterpret_cast<uint4*>(wt + (int64_t)i * rows + o0);
+    dst[0] = make_uint4(p[0], p[1], p[2], p[3]);
+    dst[1] = make_uint4(p[4], p[5], p[6], p[7]);
+  }
+}
+int dequant_bf16(const QuantPlanes& q, int rows, int cols, uint16_t* w, uint16_t* wt, hipStream_t s) {
+  SMHIP_REQUIRE(q.n == (int64_t)rows * cols, "dequant_bf16: shape does not match the planes");
+  SMHIP_REQUIRE(rows % 16 == 0 && cols % 16 == 0, "dequant_bf16: rows and cols must be multiples of 16");
+  SMHIP_REQUIRE(q.kind == SMHIP_QTYPE_Q8_0 || q.kind == SMHIP_QTYPE_Q4_K, "dequant_bf16: qtype must be Q8_0 or Q4_K");
+  SMHIP_REQUIRE(((uintptr_t)w | (uintptr_t)wt) % 16 == 0, "dequant_bf16: outputs must be 16-byte aligned");
+  if (!w && !wt) return SMHIP_OK;
+  hipLaunchKernelGGL(dequant_bf16_kernel, dim3(ceil_div(cols, 64), ceil_div(rows, 64)), dim3(256), 0, s, q, rows, cols,
+                     w, wt);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+}  // namespace smhip

@@ -1,0 +1,382 @@
+// skinny.hip — rank-sized GEMMs of the LoRA step for gfx950, streamed at HBM rate.
+//
+//   C[M, n] = alpha * sum_k Big(m, k) Small(r, k) + beta * C      (n = LoRA rank columns, <= 64)
+//
+// The four adapter products of a LoRA projection (LoRAAdapter.cs forward/backward) are all of
+// this shape: one operand is a full activation or gradient (Big, T x In or T x Out, tens of
+// MB) and the other has only n = r (or 2r, 3r for fused projections) rows:
+//   u  = x A            Big = x  [T, In]  k-contiguous, Small = A [In, n] (n contiguous)
+//   z  = dY B^T         Big = dY [T, Out] k-contiguous, Small = B [n, Out] (k contiguous)
+//   dA += s x^T z       Big = x  (k = token, m contiguous), Small = z [T, n]
+//   dB += s u^T dY      computed as its transpose dB^T[o, r] = sum_t dY[t, o] u[t, r]:
+//                       Big = dY (k = token, m contiguous), Small = u [T, n], stored transposed
+// Their cost is reading Big once, so the kernel is built for bandwidth: every workgroup
+// streams a 128-row x K/S slice of Big through a 3-stage ring of direct-to-LDS buffer loads
+// (buffer_load ... lds, two stages in flight, two workgroups per CU), and multiplies it
+// with v_mfma_f32_16x16x32_bf16 (16-column blocks: ranks 16/32/48 waste no MFMA columns).
+// Operands whose contiguous axis is m (or r) rather than k are DMA'd in their raw layout
+// (k rows) and transposed by the fragment reads (eight 16-bit LDS reads per fragment); the
+// raw Big rows are kept in 1 KiB blocks padded by 32 bytes so those column reads hit
+// distinct banks.  k-contiguous tiles use the XOR-swizzled [row][64] layout of the GEMM.
+// The reduction over K is split S ways (S chosen so the fp32 partials stay a small fraction
+// of the bytes of Big); a second kernel sums the S partials in a fixed order, so results are
+// deterministic and independent of timing.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace smhip {
+namespace sk {
+
+constexpr int MT = 128;        // Big rows per workgroup (4 waves x 32)
+constexpr int BKT = 64;        // k per stage
+constexpr int ST = 3;          // ring stages
+constexpr int RAW_BLK = 1056;  // 1 KiB of raw Big (4 k-rows of 128 m) + 32 bytes of padding
+constexpr int BIG_BYTES = 16 * RAW_BLK;  // >= 16 KiB swizzled tile
+constexpr int SMALL_BYTES = 8192;        // n <= 64 rows x 64 k x 2 bytes
+constexpr int STAGE = BIG_BYTES + SMALL_BYTES;
+constexpr uint32_t OOB = 0x80000000u;
+typedef __attribute__((address_space(3))) void lds_void;
+
+struct Args {
+  const void* big;
+  int64_t ldb;      // Big row pitch (elements)
+  int big_bytes;
+  const void* small;
+  int64_t lds;      // Small row pitch (elements)
+  int small_bytes;
+  int M, n, K;
+  int kps;          // k tiles per split
+  float* partial;   // [S][M][n] when S > 1
+  void* C;
+  int64_t ldc;
+  float alpha, beta;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+__device__ __forceinline__ int sw(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint8_t* lds, uint32_t off) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the LDS address-space cast exists only in the device pass
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)lds, 16, off, 0, 0, 0);
+#endif
+}
+template <int N>
+__device__ __forceinline__ void wait_vm_n() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Big tile loader.  BIGK: k-contiguous rows m (swizzled [128][64]); else raw k-rows.
+// Each wave issues exactly 4 DMA instructions per stage.
+template <bool BIGK>
+struct BigLoad {
+  __amdgpu_buffer_rsrc_t rs;
+  uint32_t off[4];
+  uint32_t kstep;  // bytes per k tile
+  __device__ void init(const Args& a, int m0) {
+    rs = rsrc(a.big, a.big_bytes);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int blk = j * 4 + w;
+      if constexpr (BIGK) {
+        const int r = blk * 8 + (l >> 3), c = (l & 7) ^ ((r >> 1) & 7);
+        off[j] = m0 + r < a.M ? (uint32_t)(((int64_t)(m0 + r) * a.ldb) * 2 + c * 16) : OOB;
+      } else {
+        const int kr = blk * 4 + (l >> 4);
+        off[j] = (uint32_t)(((int64_t)kr * a.ldb + m0 + (l & 15) * 8) * 2);
+      }
+    }
+    kstep = BIGK ? BKT * 2 : (uint32_t)(BKT * a.ldb * 2);
+  }
+  __device__ __forceinline__ void fetch(uint8_t* stage, int kt) {
+    const int w = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int blk = j * 4 + w;
+      dma16(rs, stage + (BIGK ? blk * 1024 : blk * RAW_BLK), off[j] == OOB ? OOB : off[j] + kt * kstep);
+    }
+  }
+  // A fragment of v_mfma_f32_16x16x32_bf16: row (lane & 15) of block rb, k = 8*(lane>>4) .. +8
+  // of k-slice kk (0..1)
+  __device__ __forceinline__ bf16x8 frag(const uint8_t* stage, int row, int kk) const {
+    const int l = threadIdx.x & 63;
+    if constexpr (BIGK) {
+      return *reinterpret_cast<const bf16x8*>(stage + sw(row, kk * 4 + (l >> 4)));
+    } else {
+      const int k0 = kk * 32 + 8 * (l >> 4);
+      bf16x8 v;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int k = k0 + j;
+        v[j] = *reinterpret_cast<const __bf16*>(stage + (k >> 2) * RAW_BLK + (k & 3) * 256 + row * 2);
+      }
+      return v;
+    }
+  }
+};
+
+// Small tile loader (n rows, n = 16 * NB).  SMALLK: k-contiguous rows (swizzled [n][64]);
+// else raw [64 k][n] (the operand's row pitch must equal n, so a tile is one contiguous
+// 128*n-byte run).  NI = n / 8 DMA instructions per tile, spread over the 4 waves; waves
+// beyond NI repeat an instruction (same bytes to the same place) so that every wave issues
+// the same count and one vmcnt value waits for a stage.
+template <bool SMALLK, int NB>
+struct SmallLoad {
+  static constexpr int N = 16 * NB;
+  static constexpr int NI = N / 8;                   // 1 KiB instructions per tile
+  static constexpr int PW = (NI + 3) / 4;            // per wave
+  __amdgpu_buffer_rsrc_t rs;
+  uint32_t off[PW];
+  int dst[PW];
+  uint32_t kstep;
+  __device__ void init(const Args& a) {
+    rs = rsrc(a.small, a.small_bytes);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < PW; j++) {
+      const int blk = (j * 4 + w) % NI;
+      dst[j] = blk * 1024;
+      if constexpr (SMALLK) {
+        const int r = blk * 8 + (l >> 3), c = (l & 7) ^ ((r >> 1) & 7);
+        off[j] = r < a.n ? (uint32_t)(((int64_t)r * a.lds) * 2 + c * 16) : OOB;
+      } else {
+        off[j] = (uint32_t)(blk * 1024 + l * 16);
+      }
+    }
+    kstep = SMALLK ? BKT * 2 : (uint32_t)(BKT * N * 2);
+  }
+  __device__ __forceinline__ void fetch(uint8_t* stage, int kt) {
+#pragma unroll
+    for (int j = 0; j < PW; j++) dma16(rs, stage + dst[j], off[j] == OOB ? OOB : off[j] + kt * kstep);
+  }
+  __device__ __forceinline__ bf16x8 frag(const uint8_t* stage, int col, int kk) const {
+    const int l = threadIdx.x & 63;
+    if constexpr (SMALLK) {
+      return *reinterpret_cast<const bf16x8*>(stage + sw(col, kk * 4 + (l >> 4)));
+    } else {
+      const int k0 = kk * 32 + 8 * (l >> 4);
+      bf16x8 v;
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = *reinterpret_cast<const __bf16*>(stage + ((k0 + j) * N + col) * 2);
+      return v;
+    }
+  }
+};
+
+template <bool BIGK, bool SMALLK, int NB, bool TRANS_OUT, bool C_BF16>
+__global__ __launch_bounds__(256, 2) void skinny_kernel(Args a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[ST * STAGE];
+  auto big_st = [&](int s) -> uint8_t* { return smem + s * STAGE; };
+  auto small_st = [&](int s) -> uint8_t* { return smem + s * STAGE + BIG_BYTES; };
+  const int m0 = blockIdx.x * MT;
+  const int split = blockIdx.y;
+  const int kt0 = split * a.kps;
+  const int nk = max(0, min(a.K / BKT, kt0 + a.kps) - kt0);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+
+  BigLoad<BIGK> lb;
+  SmallLoad<SMALLK, NB> ls;
+  lb.init(a, m0);
+  ls.init(a);
+  constexpr int PER = 4 + SmallLoad<SMALLK, NB>::PW;
+
+  floatx4 acc[2][NB];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < NB; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int t = 0; t < ST - 1; t++)
+    if (t < nk) {
+      lb.fetch(big_st(t), kt0 + t);
+      ls.fetch(small_st(t), kt0 + t);
+    }
+  for (int t = 0; t < nk; t++) {
+    if (t + ST - 2 < nk) wait_vm_n<(ST - 2) * PER>();
+    else wait_vm_n<0>();
+    ring_barrier();  // stage t landed for every wave; stage of t-1 is free
+    if (t + ST - 1 < nk) {
+      const int s = (t + ST - 1) % ST;
+      lb.fetch(big_st(s), kt0 + t + ST - 1);
+      ls.fetch(small_st(s), kt0 + t + ST - 1);
+    }
+    const uint8_t* bs = big_st(t % ST);
+    const uint8_t* ss = small_st(t % ST);
+#pragma unroll
+    for (int kk = 0; kk < BKT / 32; kk++) {
+      bf16x8 fa[2], fb[NB];
+#pragma unroll
+      for (int i = 0; i < 2; i++) fa[i] = lb.frag(bs, wv * 32 + i * 16 + (lane & 15), kk);
+#pragma unroll
+      for (int j = 0; j < NB; j++) fb[j] = ls.frag(ss, j * 16 + (lane & 15), kk);
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < NB; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // lane holds rows 4*(lane>>4) + e, column lane & 15 of each 16 x 16 block
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const int col = j * 16 + (lane & 15);
+      if (col >= a.n) continue;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int row = m0 + wv * 32 + i * 16 + 4 * (lane >> 4) + e;
+        if (row >= a.M) continue;
+        if (a.partial) {
+          a.partial[((int64_t)split * a.M + row) * a.n + col] = acc[i][j][e];
+          continue;
+        }
+        const int64_t ci = TRANS_OUT ? (int64_t)col * a.ldc + row : (int64_t)row * a.ldc + col;
+        float o = a.alpha * acc[i][j][e];
+        if constexpr (C_BF16) {
+          uint16_t* c = (uint16_t*)a.C + ci;
+          if (a.beta != 0.f) o += a.beta * bf2f(*c);
+          *c = f2bf(o);
+        } else {
+          float* c = (float*)a.C + ci;
+          if (a.beta != 0.f) o += a.beta * *c;
+          *c = o;
+        }
+      }
+    }
+}
+
+// C (m, r) = alpha * sum_s partial[s][m][r] + beta * C, splits summed in ascending order.
+// One thread per 4 consecutive r of one m (n % 16 == 0): float4 reads of the partials, which
+// are contiguous for consecutive threads; the S loads of a thread are independent and issued
+// together.
+template <bool TRANS_OUT, bool C_BF16>
+__global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restrict__ partial, int S, int M, int n,
+                                                            void* C, int64_t ldc, float alpha, float beta) {
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // float4 index
+  const int64_t total = (int64_t)M * n / 4;
+  if (q >= total) return;
+  const int n4 = n / 4;
+  const int64_t m = q / n4;
+  const int r = (int)(q - m * n4) * 4;
+  const int64_t plane = (int64_t)M * n / 4;
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const f4v* p4 = reinterpret_cast<const f4v*>(partial) + q;
+  f4v acc = {0.f, 0.f, 0.f, 0.f};
+  int sidx = 0;
+  for (; sidx + 4 <= S; sidx += 4) {
+    const f4v a0 = __builtin_nontemporal_load(p4 + (sidx + 0) * plane);
+    const f4v a1 = __builtin_nontemporal_load(p4 + (sidx + 1) * plane);
+    const f4v a2 = __builtin_nontemporal_load(p4 + (sidx + 2) * plane);
+    const f4v a3 = __builtin_nontemporal_load(p4 + (sidx + 3) * plane);
+    acc += a0;
+    acc += a1;
+    acc += a2;
+    acc += a3;
+  }
+  for (; sidx < S; sidx++) {
+    const f4v a0 = __builtin_nontemporal_load(p4 + sidx * plane);
+    acc += a0;
+  }
+  const float v[4] = {acc[0], acc[1], acc[2], acc[3]};
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int64_t ci = TRANS_OUT ? (int64_t)(r + j) * ldc + m : m * ldc + r + j;
+    float o = alpha * v[j];
+    if constexpr (C_BF16) {
+      uint16_t* c = (uint16_t*)C + ci;
+      if (beta != 0.f) o += beta * bf2f(*c);
+      *c = f2bf(o);
+    } else {
+      float* c = (float*)C + ci;
+      if (beta != 0.f) o += beta * *c;
+      *c = o;
+    }
+  }
+}
+
+template <bool BIGK, bool SMALLK, int NB>
+static void launch(const Args& a, dim3 grid, bool trans, bool cbf, hipStream_t s) {
+  if (trans) {
+    if (cbf) hipLaunchKernelGGL((skinny_kernel<BIGK, SMALLK, NB, true, true>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((skinny_kernel<BIGK, SMALLK, NB, true, false>), grid, dim3(256), 0, s, a);
+  } else {
+    if (cbf) hipLaunchKernelGGL((skinny_kernel<BIGK, SMALLK, NB, false, true>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((skinny_kernel<BIGK, SMALLK, NB, false, false>), grid, dim3(256), 0, s, a);
+  }
+}
+template <bool BIGK, bool SMALLK>
+static void launch_nb(int nb, const Args& a, dim3 grid, bool trans, bool cbf, hipStream_t s) {
+  switch (nb) {
+    case 1: launch<BIGK, SMALLK, 1>(a, grid, trans, cbf, s); break;
+    case 2: launch<BIGK, SMALLK, 2>(a, grid, trans, cbf, s); break;
+    case 3: launch<BIGK, SMALLK, 3>(a, grid, trans, cbf, s); break;
+    default: launch<BIGK, SMALLK, 4>(a, grid, trans, cbf, s); break;
+  }
+}
+
+}  // namespace sk
+
+// Returns 1 if the skinny path ran, 0 if the operands do not fit it (caller falls back to
+// the general GEMM), < 0 on error.  big_k / small_k: operand k-contiguous.  trans_out: the
+// result (m, r) is stored at C[r * ldc + m].
+int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, const void* small, int64_t lds,
+                bool small_k, float alpha, float beta, void* C, int64_t ldc, bool trans_out, bool c_bf16,
+                hipStream_t s) {
+  using namespace sk;
+  if (n < 1 || n > 64 || n % 16 || M < 1 || K < BKT || K % BKT) return 0;
+  if (((uintptr_t)big | (uintptr_t)small) % 16 || ldb % 8) return 0;
+  if (small_k && lds % 8) return 0;
+  if (!small_k && lds != n) return 0;
+  // 32-bit buffer offsets
+  const int64_t bb = big_k ? ((int64_t)(M - 1) * ldb + K) * 2 : ((int64_t)(K - 1) * ldb + M) * 2;
+  const int64_t sb = small_k ? ((int64_t)(n - 1) * lds + K) * 2 : (int64_t)K * n * 2;
+  const int64_t lim = (int64_t)1 << 31;
+  if (bb + 2 * 64 * ldb * 2 >= lim || sb + 4096 >= lim) return 0;
+  Args a{};
+  a.big = big; a.ldb = ldb; a.big_bytes = (int)bb;
+  a.small = small; a.lds = lds; a.small_bytes = (int)sb;
+  a.M = M; a.n = n; a.K = K;
+  a.C = C; a.ldc = ldc; a.alpha = alpha; a.beta = beta;
+  const int mt = ceil_div(M, MT), nk = K / BKT;
+  // splits: two workgroups per CU; fewer while the fp32 partials (written and read back)
+  // exceed a quarter of the bytes of Big, as long as every CU keeps a workgroup
+  const int cus = num_cus();
+  int S = std::max(1, ceil_div(2 * cus, mt));
+  S = std::min(S, std::max(1, nk / 2));
+  while (S > 1 && (int64_t)S * M * n * 4 * 4 > (int64_t)M * K * 2 && mt * (S - 1) >= cus) S--;
+  a.kps = ceil_div(nk, S);
+  S = ceil_div(nk, a.kps);
+  a.partial = nullptr;
+  if (S > 1) {
+    a.partial = (float*)workspace(s, sizeof(float) * (size_t)S * M * n, 7);
+    if (!a.partial) return fail(SMHIP_ENOMEM, "gemm_skinny: split workspace");
+  }
+  const dim3 grid(mt, S);
+  const int ev0 = prof_mark(s);
+  if (big_k && small_k) launch_nb<true, true>(n / 16, a, grid, trans_out, c_bf16, s);
+  else if (big_k) launch_nb<true, false>(n / 16, a, grid, trans_out, c_bf16, s);
+  else if (small_k) launch_nb<false, true>(n / 16, a, grid, trans_out, c_bf16, s);
+  else launch_nb<false, false>(n / 16, a, grid, trans_out, c_bf16, s);
+  SMHIP_CHECK_LAUNCH();
+  prof_add(PROF_GEMM, ev0, prof_mark(s), 2.0 * M * n * (double)K, M, n, K);
+  if (S > 1) {
+    const int blocks = ceil_div((int64_t)M * n / 4, 256);
+    if (trans_out) {
+      if (c_bf16) hipLaunchKernelGGL((skinny_reduce_kernel<true, true>), dim3(blocks), dim3(256), 0, s, a.partial, S, M, n, C, ldc, alpha, beta);
+      else hipLaunchKernelGGL((skinny_reduce_kernel<true, false>), dim3(blocks), dim3(256), 0, s, a.partial, S, M, n, C, ldc, alpha, beta);
+    } else {
+      if (c_bf16) hipLaunchKernelGGL((skinny_reduce_kernel<false, true>), dim3(blocks), dim3(256), 0, s, a.partial, S, M, n, C, ldc, alpha, beta);
+      else hipLaunchKernelGGL((skinny_reduce_kernel<false, false>), dim3(blocks), dim3(256), 0, s, a.partial, S, M, n, C, ldc, alpha, beta);
+    }
+    SMHIP_CHECK_LAUNCH();
+  }
+  return 1;
+}
+
+}  // namespace smhip

@@ -124,8 +124,12 @@ def test_engine_full_fp32_head128(orc, dev, neox):
     run_pair(orc, dev, c, seed=11 + neox)
 
 
+@pytest.mark.parametrize("base_ws", ["1", "0"])
 @pytest.mark.parametrize("qtype", [QTYPE_Q8_0, QTYPE_Q4_K])
-def test_engine_lora_bf16(orc, dev, qtype):
+def test_engine_lora_bf16(orc, dev, qtype, base_ws, monkeypatch):
+    """LoRA bf16 step with the frozen base decoded into the bf16 workspace each step (1) and
+    with the fused-decode GEMM loaders reading the quantised planes directly (0)."""
+    monkeypatch.setenv("SMHIP_BASE_WS", base_ws)
     c = ModelConfig(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=512, batch=2,
                     seq=128, rope_theta=1e6, rope_neox=1, qk_norm=1, base_qtype=qtype, lora_rank=8, lora_alpha=16.0,
                     precision=PREC_BF16)

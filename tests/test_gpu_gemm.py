@@ -4,7 +4,8 @@ Products of bf16 values are exact in fp32 and MFMA accumulates in fp32, so the
 bar is the fp32 one (1e-5 norm-wise) for fp32 output; bf16 output adds one
 rounding (2e-2 bar, measures ~2e-3).  Shapes cover the fast kernel (K % 64 ==
 0, both tile heights, split-K, ragged M/N edges, transposed operands) and the
-generic fallback (K not a multiple of 64).
+generic fallback (K not a multiple of 64).  split 0 is the automatic choice the engine uses
+(the 8-wave ring-buffered tile when the output has at most one 128x128 tile per CU).
 """
 import numpy as np
 import pytest
@@ -25,7 +26,8 @@ def _rnd(shape, rng):
 @pytest.mark.parametrize("M,N,K,am,bm,split", [
     (256, 256, 256, 2, 2, 1), (4096, 1024, 1024, 2, 3, 1), (300, 136, 192, 2, 3, 1), (4096, 48, 1024, 2, 3, 8),
     (48, 1024, 4096, 3, 3, 8), (1000, 32, 2048, 3, 3, 13), (8192, 512, 128, 2, 2, 1), (130, 200, 100, 2, 2, 1),
-    (64, 64, 64, 0, 1, 1)])
+    (64, 64, 64, 0, 1, 1), (4096, 1024, 1024, 2, 2, 0), (300, 136, 192, 2, 2, 0), (130, 1000, 64, 2, 2, 0),
+    (2048, 2048, 8192, 2, 2, 0)])
 @pytest.mark.parametrize("c_bf16", [0, 1])
 def test_gemm_modes(dev, M, N, K, am, bm, split, c_bf16):
     rng = np.random.default_rng(M + N + K + am + bm)
