@@ -202,7 +202,7 @@ int smhip_engine_create(const smhip_model_config* cfg, void** engine);
 int smhip_engine_destroy(void* engine);
 int smhip_engine_param_count(void* engine, int64_t* trainable, int64_t* frozen);
 int smhip_engine_set_tensor(void* engine, const char* name, const void* host, int64_t nbytes);
-/* which = 0: parameter, 1: gradient */
+/* which = 0: parameter, 1: gradient, 2: AdamW first moment m, 3: AdamW second moment v */
 int smhip_engine_get_tensor(void* engine, const char* name, int which, void* host, int64_t nbytes);
 /* Synthetic initialisation on the device: N(0,0.02) weights (quantised in LoRA mode), norms 1,
  * biases 0, LoRA A Kaiming-uniform, B ~ N(0,1e-3). */
@@ -220,6 +220,21 @@ int smhip_engine_step(void* engine, const int32_t* ids, const int32_t* labels, f
  * ids/labels into engine buffers and replay the graph on the caller's stream.  Results are
  * bit-identical to eager mode.  Calls made while the live profiler is active run eagerly. */
 int smhip_engine_use_graph(void* engine, int on);
+/* Checkpoint.Save (Checkpoint.cs:27-82) with AdamW.SaveState (Optimizers/AdamW.cs:96-105):
+ * writes <dir>/model.bin, optimizer.bin (when with_optimizer) and meta.json in the reference's
+ * byte format, creating dir.  The tensors are the reference's trainable parameter list (names,
+ * order, [In, Out] weight layout); loss NaN and note NULL are written as JSON null. */
+int smhip_engine_save_checkpoint(void* engine, const char* dir, int with_optimizer, int step, float loss,
+                                 const char* note);
+/* Checkpoint.Load (Checkpoint.cs:161-237) with AdamW.LoadState (Optimizers/AdamW.cs:107-117):
+ * tensors matched by name (repeated names in order), unknown names skipped, an element-count
+ * mismatch is an error naming the tensor.  With with_optimizer and an optimizer.bin present, m, v
+ * and lr are restored and the AdamW step becomes meta.json's step.  step / loss (nullable)
+ * receive meta.json's values (0 / NaN without one). */
+int smhip_engine_load_checkpoint(void* engine, const char* dir, int with_optimizer, int* step, float* loss);
+/* Checkpoint.FindLatest (Checkpoint.cs:117-145): path of the latest "step-*" directory under dir
+ * into out (cap bytes); returns 1 if found, 0 if none. */
+int smhip_checkpoint_find_latest(const char* dir, char* out, int64_t cap);
 /* Diagnostics: copy a saved activation of the last forward to host memory.  what: "h_in", "h_mid",
  * "xn1", "qkv", "q", "k", "v", "o", "gu", "act" (of `layer`), "h_fin", "logits" ("logits" holds
  * dLogits after a fp32-mode backward).  Element type is bf16 for "xn1|q|k|v|o|gu|act" in bf16

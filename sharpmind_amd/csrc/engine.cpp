@@ -17,7 +17,12 @@
 //    adapter of rank n*r whose B is block-diagonal; off-diagonal gradient
 //    blocks are zeroed so they stay exactly zero under AdamW.
 #include <hip/hip_runtime.h>
+#include <chrono>
 #include <cmath>
+#include <cstdio>
+#include <ctime>
+#include <filesystem>
+#include <memory>
 #include <cstring>
 #include <map>
 #include <string>
@@ -126,14 +131,19 @@ static int build(Engine* e) {
   auto add = [&](DenseRef* ref, int64_t n, bool trainable, bool decay, bool shadow) {
     (trainable ? tr : fr).push_back({ref, n, decay, shadow});
   };
+  // AdamW skips weight decay for parameters whose reference name contains "bias", "norm.weight"
+  // or "layernorm.weight" (AdamW.cs:38-41, 119-125).  The reference's parameter names are
+  // EmbeddingTable.weight, q_proj.weight ... down_proj.weight, <proj>.bias, RmsNormLayer.weight
+  // and lora.a / lora.b, so only the biases are exempt: "RmsNormLayer.weight" does not contain
+  // "norm.weight".
   const bool full = !e->lora;
   add(&e->emb, (int64_t)V * d, full, true, true);  // LoRA mode keeps emb quantised (emb_q)
-  add(&e->norm_f, d, full, false, false);
+  add(&e->norm_f, d, full, true, false);
   for (int l = 0; l < c.n_layers; l++) {
     LayerW& w = e->L[l];
-    add(&w.norm1, d, full, false, false);
-    add(&w.norm2, d, full, false, false);
-    if (c.qk_norm) { add(&w.qn, c.head_dim, full, false, false); add(&w.kn, c.head_dim, full, false, false); }
+    add(&w.norm1, d, full, true, false);
+    add(&w.norm2, d, full, true, false);
+    if (c.qk_norm) { add(&w.qn, c.head_dim, full, true, false); add(&w.kn, c.head_dim, full, true, false); }
     for (int p = 0; p < 4; p++) {
       if (full) {
         add(&w.w[p], (int64_t)e->Out[p] * e->In[p], true, true, true);
@@ -634,6 +644,316 @@ static int optimizer_step(Engine* e, hipStream_t s) {
 
 }  // namespace smhip
 
+
+// ------------------------------------------------------------------ checkpoint files
+// Checkpoint.Save / Load / ReadMeta / FindLatest (SharpMind.Training/Checkpoint.cs:27-82,
+// 90-237) and AdamW.SaveState / LoadState (Optimizers/AdamW.cs:96-117), byte-compatible:
+//   model.bin      int32 count; per tensor: int32 name length, UTF-8 name, int32 rank,
+//                  int32 dims[rank], fp32 data (little endian, the reference's row-major
+//                  [In, Out] layout for linear weights)
+//   optimizer.bin  int32 AdamW step, fp32 lr; per tensor, in the same order: m, then v
+//   meta.json      {"step", "loss" (null when NaN), "note", "savedUtc", "paramCount"}
+// The tensor list is the reference's trainable parameter list:
+//   full-parameter: Transformer.Parameters (Transformer.cs:239-260): EmbeddingTable.weight,
+//     then per block (TransformerBlock.cs:52-66) attention q_proj, k_proj, v_proj, o_proj
+//     (.weight [In, Out], .bias [Out] when biased; AttentionLayer.cs:425-433), the QK-norm
+//     weights (RmsNormLayer.weight [head_dim]), wgated_proj and down_proj (FFnLayer.cs:317-327),
+//     norm1, norm2 (RmsNormLayer.weight [d]), and last the final RmsNormLayer.weight;
+//   LoRA: per block, the adapters of q, k, v, o, gate, up, down, each lora.a [In, r] then
+//     lora.b [r, Out] (LoRALayer.cs:94-98, in LoRAAttention / LoRAFFN order).  The reference's
+//     LoRAModel holds one such set for the whole model; the engine has one per block.
+// Repeated names (RmsNormLayer.weight, lora.a, lora.b) are matched in order, as Load does.
+namespace smhip {
+
+// geometry of block blk of fused projection p: (In, Out, column offset in the fused output)
+static void block_geom(const Engine* e, int p, int blk, int* In, int* Out, int* coff) {
+  *In = e->In[p];
+  if (p == P_QKV) { const int o[3] = {0, e->qd, e->qd + e->kvd}, n[3] = {e->qd, e->kvd, e->kvd}; *Out = n[blk]; *coff = o[blk]; }
+  else if (p == P_GU) { *Out = e->c.ffn_dim; *coff = blk * e->c.ffn_dim; }
+  else { *Out = e->Out[p]; *coff = 0; }
+}
+
+struct RefParam {
+  std::string name;
+  std::vector<int> dims;
+  const DenseRef* d;
+  // element (i, j) of the reference [R][C] tensor is storage[base + i * si + j * sj]
+  int64_t base, si, sj;
+  int R, C;
+};
+
+static std::vector<RefParam> ref_params(const Engine* e) {
+  std::vector<RefParam> v;
+  const smhip_model_config& c = e->c;
+  const int d = c.d_model, F = c.ffn_dim, r = c.lora_rank;
+  auto vec = [&](const char* name, const DenseRef* t, int64_t base, int n) {
+    v.push_back({name, {n}, t, base, 0, 1, 1, n});
+  };
+  // reference [In, Out] weight = rows [off, off + Out) of an engine [Out_all][In] matrix
+  auto lin = [&](const char* name, const DenseRef* t, int In, int Out, int off) {
+    v.push_back({name, {In, Out}, t, (int64_t)off * In, 1, In, In, Out});
+  };
+  if (!e->lora) {
+    v.push_back({"EmbeddingTable.weight", {c.vocab, d}, &e->emb, 0, d, 1, c.vocab, d});
+    for (const LayerW& w : e->L) {
+      const char* qkv[3] = {"q_proj", "k_proj", "v_proj"};
+      const int off[3] = {0, e->qd, e->qd + e->kvd}, outs[3] = {e->qd, e->kvd, e->kvd};
+      for (int j = 0; j < 3; j++) {
+        lin((std::string(qkv[j]) + ".weight").c_str(), &w.w[P_QKV], d, outs[j], off[j]);
+        if (c.use_bias) vec((std::string(qkv[j]) + ".bias").c_str(), &w.b[P_QKV], off[j], outs[j]);
+      }
+      lin("o_proj.weight", &w.w[P_O], e->qd, d, 0);
+      if (c.use_bias) vec("o_proj.bias", &w.b[P_O], 0, d);
+      if (c.qk_norm) {
+        vec("RmsNormLayer.weight", &w.qn, 0, c.head_dim);
+        vec("RmsNormLayer.weight", &w.kn, 0, c.head_dim);
+      }
+      lin("wgated_proj.weight", &w.w[P_GU], d, 2 * F, 0);
+      if (c.use_bias) vec("wgated_proj.bias", &w.b[P_GU], 0, 2 * F);
+      lin("down_proj.weight", &w.w[P_D], F, d, 0);
+      if (c.use_bias) vec("down_proj.bias", &w.b[P_D], 0, d);
+      vec("RmsNormLayer.weight", &w.norm1, 0, d);
+      vec("RmsNormLayer.weight", &w.norm2, 0, d);
+    }
+    vec("RmsNormLayer.weight", &e->norm_f, 0, d);
+    return v;
+  }
+  static const int proj[7] = {P_QKV, P_QKV, P_QKV, P_O, P_GU, P_GU, P_D};
+  static const int blk[7] = {0, 1, 2, 0, 0, 1, 0};
+  for (const LayerW& w : e->L)
+    for (int t = 0; t < 7; t++) {
+      const int p = proj[t];
+      int In, Out, coff;
+      block_geom(e, p, blk[t], &In, &Out, &coff);
+      const int nr = e->nr[p], OutF = e->Out[p];
+      // A [In][nr] fused by columns; B [nr][Out_fused] block-diagonal
+      v.push_back({"lora.a", {In, r}, &w.la[p], (int64_t)blk[t] * r, nr, 1, In, r});
+      v.push_back({"lora.b", {r, Out}, &w.lb[p], (int64_t)blk[t] * r * OutF + coff, OutF, 1, r, Out});
+    }
+  return v;
+}
+
+// host copies of the parameter, m and v arenas
+struct ArenaCopy {
+  std::vector<float> a[3];
+  int get(const Engine* e) {
+    for (int k = 0; k < 3; k++) {
+      a[k].resize((size_t)std::max<int64_t>(e->n_train, 1));
+      const float* src = k == 0 ? e->train : (k == 1 ? e->m : e->v);
+      SMHIP_CHECK_HIP(hipMemcpy(a[k].data(), src, sizeof(float) * (size_t)e->n_train, hipMemcpyDeviceToHost));
+    }
+    return SMHIP_OK;
+  }
+  int put(Engine* e) const {
+    for (int k = 0; k < 3; k++) {
+      float* dst = k == 0 ? e->train : (k == 1 ? e->m : e->v);
+      SMHIP_CHECK_HIP(hipMemcpy(dst, a[k].data(), sizeof(float) * (size_t)e->n_train, hipMemcpyHostToDevice));
+    }
+    return SMHIP_OK;
+  }
+};
+
+static void gather(const Engine* e, const ArenaCopy& ac, int k, const RefParam& p, float* out) {
+  const float* st = ac.a[k].data() + (p.d->data - e->train);
+  for (int i = 0; i < p.R; i++)
+    for (int j = 0; j < p.C; j++) out[(int64_t)i * p.C + j] = st[p.base + i * p.si + j * p.sj];
+}
+static void scatter(const Engine* e, ArenaCopy& ac, int k, const RefParam& p, const float* in) {
+  float* st = ac.a[k].data() + (p.d->data - e->train);
+  for (int i = 0; i < p.R; i++)
+    for (int j = 0; j < p.C; j++) st[p.base + i * p.si + j * p.sj] = in[(int64_t)i * p.C + j];
+}
+
+static std::string json_escape(const std::string& x) {
+  std::string o;
+  for (unsigned char ch : x) {
+    if (ch == '"') o += "\\\"";
+    else if (ch == '\\') o += "\\\\";
+    else if (ch == '\n') o += "\\n";
+    else if (ch == '\r') o += "\\r";
+    else if (ch == '\t') o += "\\t";
+    else if (ch < 0x20) { char b[8]; snprintf(b, sizeof b, "\\u%04x", ch); o += b; }
+    else o += (char)ch;
+  }
+  return o;
+}
+// shortest decimal that reads back as the same float
+static std::string float_repr(float f) {
+  char b[64];
+  for (int prec = 1; prec <= 9; prec++) {
+    snprintf(b, sizeof b, "%.*g", prec, (double)f);
+    if (strtof(b, nullptr) == f) break;
+  }
+  return b;
+}
+
+struct FileCloser { void operator()(FILE* f) const { if (f) fclose(f); } };
+using File = std::unique_ptr<FILE, FileCloser>;
+
+static int save_checkpoint(Engine* e, const std::string& dir, int step, float loss, const char* note, bool with_opt) {
+  std::error_code ec;
+  std::filesystem::create_directories(dir, ec);
+  if (ec) return fail(SMHIP_EINVAL, "checkpoint: cannot create directory " + dir + ": " + ec.message());
+  SMHIP_CHECK_HIP(hipDeviceSynchronize());
+  const std::vector<RefParam> ps = ref_params(e);
+  ArenaCopy ac;
+  if (int rc = ac.get(e)) return rc;
+  std::vector<float> buf;
+  {
+    File f(fopen((dir + "/model.bin").c_str(), "wb"));
+    if (!f) return fail(SMHIP_EINVAL, "checkpoint: cannot write " + dir + "/model.bin");
+    bool ok = true;
+    auto w32 = [&](int32_t x) { ok = ok && fwrite(&x, 4, 1, f.get()) == 1; };
+    w32((int32_t)ps.size());
+    for (const RefParam& p : ps) {
+      w32((int32_t)p.name.size());
+      ok = ok && fwrite(p.name.data(), 1, p.name.size(), f.get()) == p.name.size();
+      w32((int32_t)p.dims.size());
+      for (int dd : p.dims) w32(dd);
+      buf.resize((size_t)p.R * p.C);
+      gather(e, ac, 0, p, buf.data());
+      ok = ok && fwrite(buf.data(), 4, buf.size(), f.get()) == buf.size();
+    }
+    if (!ok) return fail(SMHIP_EINVAL, "checkpoint: short write to model.bin");
+  }
+  if (with_opt) {
+    File f(fopen((dir + "/optimizer.bin").c_str(), "wb"));
+    if (!f) return fail(SMHIP_EINVAL, "checkpoint: cannot write " + dir + "/optimizer.bin");
+    const int32_t st = e->step;
+    const float lr = e->c.lr;
+    bool ok = fwrite(&st, 4, 1, f.get()) == 1 && fwrite(&lr, 4, 1, f.get()) == 1;
+    for (const RefParam& p : ps)
+      for (int k = 1; k <= 2; k++) {
+        buf.resize((size_t)p.R * p.C);
+        gather(e, ac, k, p, buf.data());
+        ok = ok && fwrite(buf.data(), 4, buf.size(), f.get()) == buf.size();
+      }
+    if (!ok) return fail(SMHIP_EINVAL, "checkpoint: short write to optimizer.bin");
+  }
+  {
+    // DateTime.UtcNow.ToString("o"): yyyy-MM-ddTHH:mm:ss.fffffffZ
+    const auto now = std::chrono::system_clock::now();
+    const auto us = std::chrono::duration_cast<std::chrono::microseconds>(now.time_since_epoch()).count();
+    const time_t secs = (time_t)(us / 1000000);
+    struct tm tmv;
+    gmtime_r(&secs, &tmv);
+    char ts[64];
+    snprintf(ts, sizeof ts, "%04d-%02d-%02dT%02d:%02d:%02d.%07lldZ", tmv.tm_year + 1900, tmv.tm_mon + 1, tmv.tm_mday,
+             tmv.tm_hour, tmv.tm_min, tmv.tm_sec, (long long)(us % 1000000) * 10);
+    std::string js = "{\n";
+    js += "  \"step\": " + std::to_string(step) + ",\n";
+    js += "  \"loss\": " + (std::isnan(loss) ? std::string("null") : float_repr(loss)) + ",\n";
+    js += "  \"note\": " + (note ? "\"" + json_escape(note) + "\"" : std::string("null")) + ",\n";
+    js += std::string("  \"savedUtc\": \"") + ts + "\",\n";
+    js += "  \"paramCount\": " + std::to_string(ps.size()) + "\n}";
+    File f(fopen((dir + "/meta.json").c_str(), "wb"));
+    if (!f || fwrite(js.data(), 1, js.size(), f.get()) != js.size())
+      return fail(SMHIP_EINVAL, "checkpoint: cannot write " + dir + "/meta.json");
+  }
+  return SMHIP_OK;
+}
+
+// the "step" and "loss" members of meta.json (ReadMeta: absent file -> step 0, loss NaN)
+static void read_meta(const std::string& dir, int* step, float* loss) {
+  *step = 0;
+  *loss = NAN;
+  File f(fopen((dir + "/meta.json").c_str(), "rb"));
+  if (!f) return;
+  std::string js;
+  char b[4096];
+  size_t n;
+  while ((n = fread(b, 1, sizeof b, f.get())) > 0) js.append(b, n);
+  auto member = [&](const char* key) -> const char* {
+    const std::string k = std::string("\"") + key + "\"";
+    size_t at = js.find(k);
+    if (at == std::string::npos) return nullptr;
+    at = js.find(':', at + k.size());
+    if (at == std::string::npos) return nullptr;
+    const char* p = js.c_str() + at + 1;
+    while (*p == ' ' || *p == '\n' || *p == '\r' || *p == '\t') p++;
+    return p;
+  };
+  if (const char* p = member("step")) *step = (int)strtol(p, nullptr, 10);
+  if (const char* p = member("loss")) {
+    if (strncmp(p, "null", 4) != 0) *loss = strtof(p, nullptr);
+  }
+}
+
+// A tensor whose element count differs from the parameter's fails the load before anything
+// reaches the device (the reference has by then overwritten the earlier parameters in place).
+static int load_checkpoint(Engine* e, const std::string& dir, bool with_opt, int* step_out, float* loss_out) {
+  std::error_code ec;
+  if (!std::filesystem::is_directory(dir, ec))
+    return fail(SMHIP_EINVAL, "checkpoint: directory not found: " + dir);
+  File f(fopen((dir + "/model.bin").c_str(), "rb"));
+  if (!f) return fail(SMHIP_EINVAL, "checkpoint: model.bin not found in " + dir);
+  SMHIP_CHECK_HIP(hipDeviceSynchronize());
+  const std::vector<RefParam> ps = ref_params(e);
+  std::map<std::string, std::vector<int>> queue;  // name -> FIFO of parameter indices
+  for (int i = (int)ps.size() - 1; i >= 0; i--) queue[ps[i].name].push_back(i);
+  ArenaCopy ac;
+  if (int rc = ac.get(e)) return rc;
+  auto r32 = [&](int32_t* x) { return fread(x, 4, 1, f.get()) == 1; };
+  int32_t count = 0;
+  if (!r32(&count) || count < 0) return fail(SMHIP_EINVAL, "checkpoint: truncated model.bin");
+  std::vector<float> buf;
+  for (int32_t t = 0; t < count; t++) {
+    int32_t len = 0, rank = 0;
+    if (!r32(&len) || len < 0 || len > (1 << 20)) return fail(SMHIP_EINVAL, "checkpoint: bad tensor name in model.bin");
+    std::string name((size_t)len, '\0');
+    if (fread(name.data(), 1, (size_t)len, f.get()) != (size_t)len || !r32(&rank) || rank < 0 || rank > 16)
+      return fail(SMHIP_EINVAL, "checkpoint: truncated model.bin");
+    int64_t elems = 1;
+    for (int k = 0; k < rank; k++) {
+      int32_t dd = 0;
+      if (!r32(&dd)) return fail(SMHIP_EINVAL, "checkpoint: truncated model.bin");
+      elems *= dd;
+    }
+    auto it = queue.find(name);
+    if (it == queue.end() || it->second.empty()) {  // not a parameter of this model: skip
+      if (fseeko(f.get(), (off_t)elems * 4, SEEK_CUR) != 0) return fail(SMHIP_EINVAL, "checkpoint: truncated model.bin");
+      continue;
+    }
+    const RefParam& p = ps[it->second.back()];
+    it->second.pop_back();
+    const int64_t have = (int64_t)p.R * p.C;
+    if (elems != have)
+      return fail(SMHIP_EINVAL, "Checkpoint tensor '" + name + "' has " + std::to_string(elems) +
+                                    " elements but the model parameter '" + p.name + "' has " + std::to_string(have) + ".");
+    buf.resize((size_t)have);
+    if (fread(buf.data(), 4, buf.size(), f.get()) != buf.size()) return fail(SMHIP_EINVAL, "checkpoint: truncated model.bin");
+    scatter(e, ac, 0, p, buf.data());
+  }
+  int step = 0;
+  float loss = NAN;
+  read_meta(dir, &step, &loss);
+  File fo(with_opt ? fopen((dir + "/optimizer.bin").c_str(), "rb") : nullptr);
+  if (fo) {  // LoadState: stored step skipped, the meta step is authoritative
+    int32_t st;
+    float lr;
+    if (fread(&st, 4, 1, fo.get()) != 1 || fread(&lr, 4, 1, fo.get()) != 1)
+      return fail(SMHIP_EINVAL, "checkpoint: truncated optimizer.bin");
+    for (const RefParam& p : ps)
+      for (int k = 1; k <= 2; k++) {
+        buf.resize((size_t)p.R * p.C);
+        if (fread(buf.data(), 4, buf.size(), fo.get()) != buf.size())
+          return fail(SMHIP_EINVAL, "checkpoint: truncated optimizer.bin");
+        scatter(e, ac, k, p, buf.data());
+      }
+    e->c.lr = lr;
+    e->step = step;
+  }
+  if (int rc = ac.put(e)) return rc;
+  if (e->train_bf)
+    if (int rc = cast_bf16(e->train, e->train_bf, e->n_train, nullptr)) return rc;
+  SMHIP_CHECK_HIP(hipDeviceSynchronize());
+  if (step_out) *step_out = step;
+  if (loss_out) *loss_out = loss;
+  return SMHIP_OK;
+}
+
+}  // namespace smhip
+
 using namespace smhip;
 
 extern "C" {
@@ -700,6 +1020,15 @@ int smhip_engine_param_count(void* engine, int64_t* trainable, int64_t* frozen) 
   return SMHIP_OK;
 }
 
+// storage of a trainable tensor: 0 parameter, 1 gradient, 2 AdamW m, 3 AdamW v (m and v
+// arenas are laid out like the parameter arena)
+static float* arena_view(const Engine* e, const DenseRef& d, int which) {
+  if (which == 0) return d.data;
+  if (which == 1) return d.grad;
+  if (!d.grad) return nullptr;
+  return (which == 2 ? e->m : e->v) + (d.data - e->train);
+}
+
 // rebuild the column planes of row planes q (bf16 LoRA engines keep both)
 static int refresh_cols(Engine* e, const QuantPlanes* q, hipStream_t s) {
   if (!e->bf || !e->lora || e->base_ws) return SMHIP_OK;
@@ -733,13 +1062,6 @@ static int lora_target(const std::string& rest, int* p, int* blk, int* isB) {
   return 0;
 }
 
-// geometry of block blk of fused projection p: (In, Out, column offset in the fused output)
-static void block_geom(const Engine* e, int p, int blk, int* In, int* Out, int* coff) {
-  *In = e->In[p];
-  if (p == P_QKV) { const int o[3] = {0, e->qd, e->qd + e->kvd}, n[3] = {e->qd, e->kvd, e->kvd}; *Out = n[blk]; *coff = o[blk]; }
-  else if (p == P_GU) { *Out = e->c.ffn_dim; *coff = blk * e->c.ffn_dim; }
-  else { *Out = e->Out[p]; *coff = 0; }
-}
 
 int smhip_engine_set_tensor(void* engine, const char* name, const void* host, int64_t nbytes) {
   SMHIP_REQUIRE(engine && name && host, "engine_set_tensor: null argument");
@@ -797,6 +1119,7 @@ int smhip_engine_set_tensor(void* engine, const char* name, const void* host, in
 
 int smhip_engine_get_tensor(void* engine, const char* name, int which, void* host, int64_t nbytes) {
   SMHIP_REQUIRE(engine && name && host, "engine_get_tensor: null argument");
+  SMHIP_REQUIRE(which >= 0 && which <= 3, "engine_get_tensor: which must be 0 (parameter), 1 (gradient), 2 (AdamW m), 3 (AdamW v)");
   Engine* e = (Engine*)engine;
   SMHIP_CHECK_HIP(hipDeviceSynchronize());
   const int r = e->c.lora_rank;
@@ -806,7 +1129,8 @@ int smhip_engine_get_tensor(void* engine, const char* name, int which, void* hos
     int In, Out, coff;
     block_geom(e, p, blk, &In, &Out, &coff);
     LayerW& w = e->L[layer];
-    const float* base = which ? (isB ? w.lb[p].grad : w.la[p].grad) : (isB ? w.lb[p].data : w.la[p].data);
+    const DenseRef& dr = isB ? w.lb[p] : w.la[p];
+    const float* base = arena_view(e, dr, which);
     if (!isB) {
       SMHIP_REQUIRE(nbytes == (int64_t)In * r * 4, "engine_get_tensor: LoRA A size mismatch");
       SMHIP_CHECK_HIP(hipMemcpy2D(host, sizeof(float) * r, base + blk * r, sizeof(float) * e->nr[p], sizeof(float) * r,
@@ -822,8 +1146,8 @@ int smhip_engine_get_tensor(void* engine, const char* name, int which, void* hos
   SMHIP_REQUIRE(it != e->dense_by_name.end(), std::string("engine_get_tensor: unknown tensor ") + name);
   DenseRef* d = it->second;
   SMHIP_REQUIRE(nbytes == d->n * 4, std::string("engine_get_tensor: size mismatch for ") + name);
-  const float* src = which ? d->grad : d->data;
-  SMHIP_REQUIRE(src, std::string("engine_get_tensor: no gradient for frozen tensor ") + name);
+  SMHIP_REQUIRE(which == 0 || d->grad, std::string("engine_get_tensor: no gradient or optimizer state for frozen tensor ") + name);
+  const float* src = arena_view(e, *d, which);
   SMHIP_CHECK_HIP(hipMemcpy(host, src, nbytes, hipMemcpyDeviceToHost));
   return SMHIP_OK;
 }
@@ -999,6 +1323,43 @@ int smhip_fill_token_ids(int32_t* ids, int64_t n, uint64_t seed, int vocab, smhi
 int smhip_quantize(int qtype, const float* x, int64_t n, void* out, smhip_stream_t stream) {
   SMHIP_REQUIRE(x && out && n >= 0, "quantize: bad arguments");
   return encode_quant(qtype, x, n, out, (hipStream_t)stream);
+}
+
+
+int smhip_engine_save_checkpoint(void* engine, const char* dir, int with_optimizer, int step, float loss,
+                                 const char* note) {
+  SMHIP_REQUIRE(engine && dir && *dir, "engine_save_checkpoint: null argument");
+  return save_checkpoint((Engine*)engine, dir, step, loss, note, with_optimizer != 0);
+}
+
+int smhip_engine_load_checkpoint(void* engine, const char* dir, int with_optimizer, int* step, float* loss) {
+  SMHIP_REQUIRE(engine && dir && *dir, "engine_load_checkpoint: null argument");
+  return load_checkpoint((Engine*)engine, dir, with_optimizer != 0, step, loss);
+}
+
+int smhip_checkpoint_find_latest(const char* dir, char* out, int64_t cap) {
+  SMHIP_REQUIRE(out && cap > 0, "checkpoint_find_latest: null output");
+  out[0] = '\0';
+  if (!dir || !*dir) return 0;
+  std::error_code ec;
+  if (!std::filesystem::is_directory(dir, ec)) return 0;
+  // Checkpoint.FindLatest compares parsed steps (Checkpoint.cs:117-134), but its ParseStep
+  // returns 0 for every name that starts with "step-" (Checkpoint.cs:138-145), so every candidate ties and the
+  // ordinal-greatest directory name wins; that is the behaviour reproduced here (for the
+  // zero-padded names TrainLoop writes it is also the highest step)
+  std::string best;
+  for (const auto& ent : std::filesystem::directory_iterator(dir, ec)) {
+    std::error_code ec2;
+    if (!ent.is_directory(ec2)) continue;
+    const std::string name = ent.path().filename().string();
+    if (name.rfind("step-", 0) != 0) continue;
+    if (best.empty() || name.compare(best) > 0) best = name;
+  }
+  if (best.empty()) return 0;
+  const std::string path = (std::filesystem::path(dir) / best).string();
+  SMHIP_REQUIRE((int64_t)path.size() < cap, "checkpoint_find_latest: output buffer too small");
+  memcpy(out, path.c_str(), path.size() + 1);
+  return 1;
 }
 
 }  // extern "C"

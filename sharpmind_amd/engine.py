@@ -60,10 +60,24 @@ class Engine:
         a = np.ascontiguousarray(arr)
         check(lib().smhip_engine_set_tensor(self.h, name.encode(), a.ctypes.data, a.nbytes))
 
-    def get(self, name, shape, grad=False):
+    def get(self, name, shape, grad=False, state=None):
+        """Parameter (default), its gradient (grad=True) or AdamW state (state='m' | 'v')."""
+        which = {None: 1 if grad else 0, "m": 2, "v": 3}[state]
         out = np.zeros(shape, np.float32)
-        check(lib().smhip_engine_get_tensor(self.h, name.encode(), 1 if grad else 0, out.ctypes.data, out.nbytes))
+        check(lib().smhip_engine_get_tensor(self.h, name.encode(), which, out.ctypes.data, out.nbytes))
         return out
+
+    def save_checkpoint(self, directory, step=0, loss=float("nan"), note=None, optimizer=True):
+        """Checkpoint.Save (Checkpoint.cs:27-82): model.bin, optimizer.bin, meta.json."""
+        check(lib().smhip_engine_save_checkpoint(self.h, str(directory).encode(), 1 if optimizer else 0, int(step),
+                                                 float(loss), note.encode() if note is not None else None))
+
+    def load_checkpoint(self, directory, optimizer=True):
+        """Checkpoint.Load (Checkpoint.cs:161-237); returns meta.json's (step, loss)."""
+        st, ls = ctypes.c_int(), ctypes.c_float()
+        check(lib().smhip_engine_load_checkpoint(self.h, str(directory).encode(), 1 if optimizer else 0,
+                                                 ctypes.byref(st), ctypes.byref(ls)))
+        return st.value, ls.value
 
     def init_synthetic(self, seed=0):
         check(lib().smhip_engine_init_synthetic(self.h, seed))
@@ -87,6 +101,15 @@ class Engine:
     def step(self, ids, labels, loss=None):
         check(lib().smhip_engine_step(self.h, ids.data_ptr(), labels.data_ptr(),
                                       loss.data_ptr() if loss is not None else None, self._stream()))
+
+
+def find_latest_checkpoint(directory):
+    """Checkpoint.FindLatest (Checkpoint.cs:117-145): latest step-* directory, or None."""
+    buf = ctypes.create_string_buffer(4096)
+    rc = lib().smhip_checkpoint_find_latest(str(directory).encode() if directory is not None else None, buf, len(buf))
+    if rc < 0:
+        check(rc)
+    return buf.value.decode() if rc == 1 else None
 
 
 def next_token_labels(ids, seq):

@@ -269,3 +269,25 @@ def test_engine_graph_replay_matches_eager(orc, dev):
             got = grads()
             for n in got:
                 assert np.array_equal(got[n], ref[i][1][n]), (rep, i, n)
+
+
+def test_engine_full_optimizer_decay_groups(orc, dev):
+    """Full-parameter AdamW with weight decay: biases are exempt and norm weights decay, as the
+    reference's name rule gives for its parameter names (AdamW.cs:38-41, 119-125)."""
+    c = ModelConfig(n_layers=1, d_model=128, n_heads=4, n_kv_heads=2, head_dim=32, ffn_dim=192, vocab=256, batch=1,
+                    seq=64, rope_theta=1e4, rope_neox=0, qk_norm=1, use_bias=1, precision=PREC_FP32)
+    eng, P, G = build(orc, c, 5)
+    ids = torch.from_numpy(np.random.default_rng(2).integers(0, c.vocab, c.tokens).astype(np.int32)).to(dev)
+    eng.forward_backward(ids, next_token_labels(ids, c.seq))
+    specs = tensor_specs(c)
+    before = {n: eng.get(n, s) for n, s, _ in specs}
+    grads = {n: eng.get(n, s, grad=True) for n, s, _ in specs}
+    eng.optimizer_step()
+    bc1 = float(np.float32(1) - np.float32(0.9))
+    bc2 = float(np.float32(1) - np.float32(0.95))
+    for n, s, kind in specs:
+        ref = before[n].copy().ravel()
+        m, v = np.zeros_like(ref), np.zeros_like(ref)
+        decay = 0.0 if kind == "bias" else 0.1
+        orc.orc_adamw(ref, np.ascontiguousarray(grads[n].ravel()), m, v, ref.size, 0.9, 0.95, bc1, bc2, 1e-3, 1e-8, decay)
+        assert np.array_equal(eng.get(n, s).ravel(), ref), n
