@@ -235,6 +235,16 @@ int smhip_engine_load_checkpoint(void* engine, const char* dir, int with_optimiz
 /* Checkpoint.FindLatest (Checkpoint.cs:117-145): path of the latest "step-*" directory under dir
  * into out (cap bytes); returns 1 if found, 0 if none. */
 int smhip_checkpoint_find_latest(const char* dir, char* out, int64_t cap);
+/* GgufLoader.LoadAllWeights / LoadSingleTensor (SharpMind.Model/Format/GgufLoader.cs:435-600) for a LoRA engine's frozen
+ * base: token_embd, blk.<i>.attn_q|attn_k|attn_v|attn_output|ffn_gate|ffn_up|ffn_down.weight (ggml type
+ * = base_qtype), the norms attn_norm, ffn_norm, attn_q_norm, attn_k_norm, output_norm (F32 or F16).
+ * Names, types and shapes are checked against the engine; an untied output.weight is an error. */
+int smhip_engine_load_gguf(void* engine, const char* path);
+/* GGUF header inspection (GgufLoader.LoadMeta, GgufLoader.cs:124-177): the tensor table of a file.
+ * dims receives 8 entries (innermost first, padded with 1); file_offset is absolute. */
+int smhip_gguf_tensor_count(const char* path, int64_t* count);
+int smhip_gguf_tensor_info(const char* path, int64_t index, char* name, int64_t cap, int* ggml_type, int* n_dims,
+                           int64_t* dims, int64_t* file_offset);
 /* Diagnostics: copy a saved activation of the last forward to host memory.  what: "h_in", "h_mid",
  * "xn1", "qkv", "q", "k", "v", "o", "gu", "act" (of `layer`), "h_fin", "logits" ("logits" holds
  * dLogits after a fp32-mode backward).  Element type is bf16 for "xn1|q|k|v|o|gu|act" in bf16

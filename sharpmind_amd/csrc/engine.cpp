@@ -29,6 +29,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "gguf.hpp"
 #include "kernels.hpp"
 
 namespace smhip {
@@ -1360,6 +1361,101 @@ int smhip_checkpoint_find_latest(const char* dir, char* out, int64_t cap) {
   SMHIP_REQUIRE((int64_t)path.size() < cap, "checkpoint_find_latest: output buffer too small");
   memcpy(out, path.c_str(), path.size() + 1);
   return 1;
+}
+
+
+// GgufLoader.LoadAllWeights / LoadSingleTensor (SharpMind.Model/Format/GgufLoader.cs:435-600) for
+// the frozen base of a LoRA engine: the standard llama.cpp tensor names, raw quantised bytes
+// handed to set_tensor unchanged (q|k|v and gate|up rows concatenated: each row is whole
+// blocks, so the fused matrix is the byte concatenation), norms from F32 or F16.
+int smhip_engine_load_gguf(void* engine, const char* path) {
+  SMHIP_REQUIRE(engine && path, "engine_load_gguf: null argument");
+  Engine* e = (Engine*)engine;
+  SMHIP_REQUIRE(e->lora, "engine_load_gguf: GGUF supplies the frozen quantised base of a LoRA engine (base_qtype Q8_0 or Q4_K)");
+  GgufFile g;
+  if (int rc = gguf_parse(path, &g)) return rc;
+  const smhip_model_config& c = e->c;
+  const int d = c.d_model, F = c.ffn_dim, D = c.head_dim;
+  const uint32_t qt = (uint32_t)c.base_qtype;
+  if (const std::string* arch = g.string_value("general.architecture")) {
+    int64_t blocks;
+    if (g.int_value(*arch + ".block_count", &blocks))
+      SMHIP_REQUIRE(blocks == c.n_layers, "engine_load_gguf: file has " + std::to_string(blocks) +
+                                              " blocks, the engine " + std::to_string(c.n_layers));
+  }
+  SMHIP_REQUIRE(!g.find("output.weight"),
+                "engine_load_gguf: the file has an untied output.weight; the engine's LM head is tied to token_embd");
+  struct Closer { void operator()(FILE* f) const { if (f) fclose(f); } };
+  std::unique_ptr<FILE, Closer> f(fopen(path, "rb"));
+  SMHIP_REQUIRE(f, std::string("engine_load_gguf: cannot open ") + path);
+  auto tname = [](const char* fmt, int l) {
+    char b[128];
+    snprintf(b, sizeof b, fmt, l);
+    return std::string(b);
+  };
+  // appends the raw bytes of tensor `name` (type `type`, dims innermost first) to buf
+  auto read = [&](const std::string& name, uint32_t type, std::vector<int64_t> dims, std::vector<uint8_t>* buf) -> int {
+    const GgufTensor* t = g.find(name);
+    SMHIP_REQUIRE(t, "engine_load_gguf: missing tensor " + name);
+    SMHIP_REQUIRE(t->type == type, "engine_load_gguf: " + name + " has ggml type " + std::to_string(t->type) +
+                                       ", expected " + std::to_string(type));
+    SMHIP_REQUIRE(t->dims == dims, "engine_load_gguf: " + name + " has an unexpected shape");
+    const int64_t bytes = gguf_tensor_bytes(type, dims);
+    SMHIP_REQUIRE(bytes > 0, "engine_load_gguf: unsupported layout for " + name);
+    const size_t at = buf->size();
+    buf->resize(at + (size_t)bytes);
+    if (fseeko(f.get(), (off_t)(g.data_offset + t->offset), SEEK_SET) != 0 ||
+        fread(buf->data() + at, 1, (size_t)bytes, f.get()) != (size_t)bytes)
+      return fail(SMHIP_EINVAL, "engine_load_gguf: truncated data for " + name);
+    return SMHIP_OK;
+  };
+  auto set = [&](const std::string& name, const std::vector<uint8_t>& buf) {
+    return smhip_engine_set_tensor(engine, name.c_str(), buf.data(), (int64_t)buf.size());
+  };
+  auto norm = [&](const std::string& gname, int n, const std::string& ename) -> int {
+    const GgufTensor* t = g.find(gname);
+    SMHIP_REQUIRE(t, "engine_load_gguf: missing tensor " + gname);
+    SMHIP_REQUIRE(t->type == 0 || t->type == 1, "engine_load_gguf: " + gname + " must be F32 or F16");
+    std::vector<uint8_t> raw;
+    if (int rc = read(gname, t->type, {n}, &raw)) return rc;
+    std::vector<float> w((size_t)n);
+    for (int i = 0; i < n; i++) {
+      if (t->type == 0) memcpy(&w[i], raw.data() + 4 * i, 4);
+      else w[i] = half_bits_to_float((uint16_t)(raw[2 * i] | (raw[2 * i + 1] << 8)));
+    }
+    return smhip_engine_set_tensor(engine, ename.c_str(), w.data(), (int64_t)n * 4);
+  };
+  std::vector<uint8_t> buf;
+  int rc;
+  if ((rc = read("token_embd.weight", qt, {d, c.vocab}, &buf)) || (rc = set("emb", buf))) return rc;
+  if ((rc = norm("output_norm.weight", d, "norm_f"))) return rc;
+  for (int l = 0; l < c.n_layers; l++) {
+    for (const char* b : {"blk.%d.attn_q.bias", "blk.%d.attn_k.bias", "blk.%d.attn_v.bias", "blk.%d.attn_output.bias"})
+      SMHIP_REQUIRE(!g.find(tname(b, l)), "engine_load_gguf: linear biases are not supported by LoRA engines (" +
+                                              tname(b, l) + ")");
+    buf.clear();
+    if ((rc = read(tname("blk.%d.attn_q.weight", l), qt, {d, e->qd}, &buf)) ||
+        (rc = read(tname("blk.%d.attn_k.weight", l), qt, {d, e->kvd}, &buf)) ||
+        (rc = read(tname("blk.%d.attn_v.weight", l), qt, {d, e->kvd}, &buf)) || (rc = set(tname("l%d.wqkv", l), buf)))
+      return rc;
+    buf.clear();
+    if ((rc = read(tname("blk.%d.attn_output.weight", l), qt, {e->qd, d}, &buf)) || (rc = set(tname("l%d.wo", l), buf)))
+      return rc;
+    buf.clear();
+    if ((rc = read(tname("blk.%d.ffn_gate.weight", l), qt, {d, F}, &buf)) ||
+        (rc = read(tname("blk.%d.ffn_up.weight", l), qt, {d, F}, &buf)) || (rc = set(tname("l%d.wgu", l), buf)))
+      return rc;
+    buf.clear();
+    if ((rc = read(tname("blk.%d.ffn_down.weight", l), qt, {F, d}, &buf)) || (rc = set(tname("l%d.wd", l), buf)))
+      return rc;
+    if ((rc = norm(tname("blk.%d.attn_norm.weight", l), d, tname("l%d.norm1", l))) ||
+        (rc = norm(tname("blk.%d.ffn_norm.weight", l), d, tname("l%d.norm2", l))))
+      return rc;
+    if (c.qk_norm && ((rc = norm(tname("blk.%d.attn_q_norm.weight", l), D, tname("l%d.q_norm", l))) ||
+                      (rc = norm(tname("blk.%d.attn_k_norm.weight", l), D, tname("l%d.k_norm", l)))))
+      return rc;
+  }
+  return SMHIP_OK;
 }
 
 }  // extern "C"

@@ -67,6 +67,10 @@ class Engine:
         check(lib().smhip_engine_get_tensor(self.h, name.encode(), which, out.ctypes.data, out.nbytes))
         return out
 
+    def load_gguf(self, path):
+        """Frozen quantised base from a GGUF file (GgufLoader.LoadAllWeights, GgufLoader.cs:435-600)."""
+        check(lib().smhip_engine_load_gguf(self.h, str(path).encode()))
+
     def save_checkpoint(self, directory, step=0, loss=float("nan"), note=None, optimizer=True):
         """Checkpoint.Save (Checkpoint.cs:27-82): model.bin, optimizer.bin, meta.json."""
         check(lib().smhip_engine_save_checkpoint(self.h, str(directory).encode(), 1 if optimizer else 0, int(step),
@@ -101,6 +105,21 @@ class Engine:
     def step(self, ids, labels, loss=None):
         check(lib().smhip_engine_step(self.h, ids.data_ptr(), labels.data_ptr(),
                                       loss.data_ptr() if loss is not None else None, self._stream()))
+
+
+def gguf_tensor_table(path):
+    """[(name, dims innermost first, ggml type, absolute file offset)] of a GGUF file."""
+    n = ctypes.c_int64()
+    check(lib().smhip_gguf_tensor_count(str(path).encode(), ctypes.byref(n)))
+    out = []
+    for i in range(n.value):
+        name = ctypes.create_string_buffer(1024)
+        t, nd, off = ctypes.c_int(), ctypes.c_int(), ctypes.c_int64()
+        dims = (ctypes.c_int64 * 8)()
+        check(lib().smhip_gguf_tensor_info(str(path).encode(), i, name, len(name), ctypes.byref(t), ctypes.byref(nd),
+                                           dims, ctypes.byref(off)))
+        out.append((name.value.decode(), tuple(dims[:nd.value]), t.value, off.value))
+    return out
 
 
 def find_latest_checkpoint(directory):
