@@ -102,7 +102,8 @@ def elementwise_hbm(L, dev, reps=20):
 
 
 def gemm_dx_traffic():
-    """HBM bytes per launch of the backward dX GEMMs, measured offline with rocprofv3 --pmc
+    """HBM bytes per launch of the backward dX GEMMs (kernel instantiations with TAG 1), measured
+    offline with rocprofv3 --pmc
     (FETCH_SIZE and WRITE_SIZE runs, scaled by a device-copy calibration); the summary with
     the commands is profiles/gemm_dx_traffic_lora_q8_qwen3_0.6b_4x1024.md.  None if absent."""
     path = os.path.join(ROOT, "profiles", "gemm_dx_traffic_lora_q8_qwen3_0.6b_4x1024.md")
@@ -231,7 +232,8 @@ def main():
     tf = lambda fl, ms: round(fl / (ms * 1e-3) / 1e12, 2) if ms else None
     if dx_n:  # dominant kernel: the backward dX GEMMs through the frozen quantised base
         k_ms, k_n, k_fl = dx_ms, dx_n, dx_fl
-        kname = "gemm_kernel, B = quantised base column planes (backward dX = dY W, bf16 MFMA)"
+        kname = ("gemm_kernel<..., TAG 1>: backward dX = dY W through the frozen base (bf16 copy decoded "
+                 "from Q8_0 each step), bf16 MFMA")
     else:
         k_ms, k_n, k_fl = all_ms, all_n, all_fl
         kname = "gemm_kernel (all linears, fwd+bwd)"

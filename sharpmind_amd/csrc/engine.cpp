@@ -82,6 +82,9 @@ struct Engine {
   // straight to LDS; without room for it the GEMMs decode the codes in their loaders
   bool base_ws = false;
   uint16_t *emb_b = nullptr, *emb_bt = nullptr;
+  DequantJob* dq_jobs = nullptr;  // device table of the per-step decode (one launch)
+  int dq_njobs = 0;
+  int64_t dq_tiles = 0;
   std::vector<LayerW> L;
   std::map<std::string, DenseRef*> dense_by_name;
   // activations
@@ -239,6 +242,21 @@ static int build(Engine* e) {
           if (int rc = bfbuf(&e->L[l].wb[p], (int64_t)e->Out[p] * e->In[p])) return rc;
           if (int rc = bfbuf(&e->L[l].wbt[p], (int64_t)e->Out[p] * e->In[p])) return rc;
         }
+      std::vector<DequantJob> jobs;
+      auto job = [&](const QuantPlanes& q, int rows, int cols, uint16_t* w, uint16_t* wt) -> int {
+        if (int rc = dequant_bf16_check(q, rows, cols, w, wt)) return rc;
+        jobs.push_back({q, rows, cols, w, wt, e->dq_tiles});
+        e->dq_tiles += (int64_t)ceil_div(rows, 64) * ceil_div(cols, 64);
+        return SMHIP_OK;
+      };
+      if (int rc = job(e->emb_q, V, d, e->emb_b, e->emb_bt)) return rc;
+      for (int l = 0; l < c.n_layers; l++)
+        for (int p = 0; p < 4; p++)
+          if (int rc = job(e->L[l].q[p], e->Out[p], e->In[p], e->L[l].wb[p], e->L[l].wbt[p])) return rc;
+      e->dq_njobs = (int)jobs.size();
+      e->dq_jobs = (DequantJob*)dalloc(e, sizeof(DequantJob) * jobs.size());
+      if (!e->dq_jobs) return fail(SMHIP_ENOMEM, "engine: decode table");
+      SMHIP_CHECK_HIP(hipMemcpy(e->dq_jobs, jobs.data(), sizeof(DequantJob) * jobs.size(), hipMemcpyHostToDevice));
     } else if (e->bf) {  // column planes for the bf16 dX GEMMs
       void* emb_t = nullptr;
       if (int rc = mk(&e->emb_qt, &emb_t, (int64_t)V * d)) return rc;
@@ -506,11 +524,8 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
 #define R_(x) do { if ((rc = (x))) return rc; } while (0)
   R_(zero_bytes(e->grad, sizeof(float) * (size_t)e->n_train, s));  // optimizer.ZeroGrad (TrainLoop.cs:109)
 
-  if (e->base_ws) {  // decode the frozen base into the bf16 workspace (both layouts)
-    R_(dequant_bf16(e->emb_q, V, d, e->emb_b, e->emb_bt, s));
-    for (int l = 0; l < c.n_layers; l++)
-      for (int p = 0; p < 4; p++) R_(dequant_bf16(e->L[l].q[p], e->Out[p], e->In[p], e->L[l].wb[p], e->L[l].wbt[p], s));
-  }
+  // decode the frozen base into the bf16 workspace (both layouts), all matrices in one launch
+  if (e->base_ws) R_(dequant_bf16_many(e->dq_jobs, e->dq_njobs, e->dq_tiles, s));
 
   // ---------------- forward
   if (e->lora) {

@@ -371,7 +371,9 @@ struct Shape {
   static constexpr int OCC = LDS * 2 <= 160 * 1024 && MB * NB <= 8 && NW == 4 ? 2 : 1;
 };
 
-template <int BM, int BN, int WGM, int NW, int AMODE, int BMODE, bool C_BF16, int ST = 2>
+// TAG only names the instantiation (1: the backward dX products through the frozen base, so
+// profilers can tell them from the forward GEMMs that share the code)
+template <int BM, int BN, int WGM, int NW, int AMODE, int BMODE, bool C_BF16, int ST = 2, int TAG = 0>
 __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW, ST>::OCC)) void gemm_kernel(Args g) {
   using S = Shape<BM, BN, WGM, NW, ST>;
   constexpr int NT = S::NT;
@@ -632,43 +634,46 @@ static int ring_stages(int nw) {
   static const int v = [] { const char* e = getenv("SMHIP_GEMM_STAGES"); return e ? atoi(e) : 0; }();
   return v ? v : (nw == 8 ? 3 : 2);
 }
-template <int BM, int BN, int WGM, int NW, int AM, int BMD>
+template <int BM, int BN, int WGM, int NW, int AM, int BMD, int TAG>
 static void launch_c(const Args& a, int c_bf16, int splits, hipStream_t s) {
   const dim3 grid(a.tiles_m * a.tiles_n, splits);
   if constexpr (AM == SRC_BF16_K && BMD == SRC_BF16_K && BM + BN <= 256) {
     const int st = ring_stages(NW);
     if (st == 3 || st == 4) {
       if (c_bf16 && !a.partial) {
-        if (st == 3) hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, true, 3>), grid, dim3(64 * NW), 0, s, a);
-        else hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, true, 4>), grid, dim3(64 * NW), 0, s, a);
+        if (st == 3) hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, true, 3, TAG>), grid, dim3(64 * NW), 0, s, a);
+        else hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, true, 4, TAG>), grid, dim3(64 * NW), 0, s, a);
       } else {
-        if (st == 3) hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, false, 3>), grid, dim3(64 * NW), 0, s, a);
-        else hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, false, 4>), grid, dim3(64 * NW), 0, s, a);
+        if (st == 3) hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, false, 3, TAG>), grid, dim3(64 * NW), 0, s, a);
+        else hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, false, 4, TAG>), grid, dim3(64 * NW), 0, s, a);
       }
       return;
     }
   }
-  if (c_bf16 && !a.partial) hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, true>), grid, dim3(64 * NW), 0, s, a);
-  else hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, false>), grid, dim3(64 * NW), 0, s, a);
+  if (c_bf16 && !a.partial) hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, true, 2, TAG>), grid, dim3(64 * NW), 0, s, a);
+  else hipLaunchKernelGGL((gemm_kernel<BM, BN, WGM, NW, AM, BMD, false, 2, TAG>), grid, dim3(64 * NW), 0, s, a);
 }
 
-template <int AM, int BMD>
+template <int AM, int BMD, int TAG = 0>
 static void launch_tile(int tile, const Args& a, int c_bf16, int sp, hipStream_t s) {
   switch (tile) {
-    case T256x256: launch_c<256, 256, 2, 8, AM, BMD>(a, c_bf16, sp, s); break;
-    case T256x128: launch_c<256, 128, 2, 4, AM, BMD>(a, c_bf16, sp, s); break;
-    case T128x128: launch_c<128, 128, 2, 4, AM, BMD>(a, c_bf16, sp, s); break;
-    case T256x64: launch_c<256, 64, 4, 4, AM, BMD>(a, c_bf16, sp, s); break;
-    case T64x128: launch_c<64, 128, 1, 4, AM, BMD>(a, c_bf16, sp, s); break;
-    case T128x128W8: launch_c<128, 128, 2, 8, AM, BMD>(a, c_bf16, sp, s); break;
-    default: launch_c<128, 64, 4, 4, AM, BMD>(a, c_bf16, sp, s); break;
+    case T256x256: launch_c<256, 256, 2, 8, AM, BMD, TAG>(a, c_bf16, sp, s); break;
+    case T256x128: launch_c<256, 128, 2, 4, AM, BMD, TAG>(a, c_bf16, sp, s); break;
+    case T128x128: launch_c<128, 128, 2, 4, AM, BMD, TAG>(a, c_bf16, sp, s); break;
+    case T256x64: launch_c<256, 64, 4, 4, AM, BMD, TAG>(a, c_bf16, sp, s); break;
+    case T64x128: launch_c<64, 128, 1, 4, AM, BMD, TAG>(a, c_bf16, sp, s); break;
+    case T128x128W8: launch_c<128, 128, 2, 8, AM, BMD, TAG>(a, c_bf16, sp, s); break;
+    default: launch_c<128, 64, 4, 4, AM, BMD, TAG>(a, c_bf16, sp, s); break;
   }
 }
 
-static bool dispatch(int tile, const Args& a, int amode, int bmode, int c_bf16, int sp, hipStream_t s) {
+static bool dispatch(int tile, const Args& a, int amode, int bmode, int c_bf16, int sp, bool dx, hipStream_t s) {
   if (amode == SRC_BF16_K) {
     switch (bmode) {
-      case SRC_BF16_K: launch_tile<SRC_BF16_K, SRC_BF16_K>(tile, a, c_bf16, sp, s); return true;
+      case SRC_BF16_K:
+        if (dx) launch_tile<SRC_BF16_K, SRC_BF16_K, 1>(tile, a, c_bf16, sp, s);
+        else launch_tile<SRC_BF16_K, SRC_BF16_K>(tile, a, c_bf16, sp, s);
+        return true;
       case SRC_BF16_R: launch_tile<SRC_BF16_K, SRC_BF16_R>(tile, a, c_bf16, sp, s); return true;
       case SRC_Q8_K: launch_tile<SRC_BF16_K, SRC_Q8_K>(tile, a, c_bf16, sp, s); return true;
       case SRC_Q8T: launch_tile<SRC_BF16_K, SRC_Q8T>(tile, a, c_bf16, sp, s); return true;
@@ -824,7 +829,7 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
     if (!a.partial) return fail(SMHIP_ENOMEM, "gemm: split-K workspace");
   }
   const int ev0 = prof_mark(s);
-  if (!dispatch(tile, a, am, bm, g.c_bf16, sp, s)) return 0;
+  if (!dispatch(tile, a, am, bm, g.c_bf16, sp, g.prof_cat == PROF_GEMM_DX, s)) return 0;
   SMHIP_CHECK_LAUNCH();
   prof_add(g.prof_cat ? g.prof_cat : (bm == SRC_Q8T || bm == SRC_Q4KT ? PROF_GEMM_DX : PROF_GEMM), ev0, prof_mark(s),
            2.0 * g.M * g.N * ((double)g.K + g.K2), g.M, g.N, g.K + g.K2);

@@ -49,7 +49,16 @@ size_t planes_bytes(int qtype, int64_t n, size_t* qs_bytes);
 int repack_planes(int qtype, const void* raw, int64_t n, void* dst, QuantPlanes* out, hipStream_t s);
 int dequant_rows(const QuantPlanes& q, const int32_t* ids, float* out, int T, int D, hipStream_t s);
 int make_col_planes(const QuantPlanes& q, int rows, int cols, void* dst, QuantPlanes* out, hipStream_t s);
-int dequant_bf16(const QuantPlanes& q, int rows, int cols, uint16_t* w, uint16_t* wt, hipStream_t s);
+// one launch decoding many matrices; `first` = index of the job's first 64x64 tile in the grid
+struct DequantJob {
+  QuantPlanes q;
+  int rows, cols;
+  uint16_t* w;
+  uint16_t* wt;
+  int64_t first;
+};
+int dequant_bf16_check(const QuantPlanes& q, int rows, int cols, const uint16_t* w, const uint16_t* wt);
+int dequant_bf16_many(const DequantJob* jobs_dev, int njobs, int64_t total_tiles, hipStream_t s);
 
 // attention.hip
 int attention_slot_backward(const float* dO, const float* q, const float* k, const float* v,

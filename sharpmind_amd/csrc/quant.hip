@@ -235,11 +235,10 @@ namespace smhip {
 // each thread decodes 16 consecutive elements of one row (one 16-byte code load, one scale),
 // writes them to the row layout and to an LDS tile, from which 16 consecutive rows of one
 // column are written to the transposed layout.
-__global__ __launch_bounds__(256) void dequant_bf16_kernel(QuantPlanes q, int rows, int cols,
-                                                           uint16_t* __restrict__ w, uint16_t* __restrict__ wt) {
-  __shared__ uint16_t tile[64][64 + 2];
+__device__ __forceinline__ void dequant_bf16_tile(const QuantPlanes& q, int rows, int cols, uint16_t* __restrict__ w,
+                                                  uint16_t* __restrict__ wt, int bx, int by, uint16_t (*tile)[66]) {
   const int tr = threadIdx.x >> 2, tc = (threadIdx.x & 3) * 16;
-  const int o = blockIdx.y * 64 + tr, i0 = blockIdx.x * 64 + tc;
+  const int o = by * 64 + tr, i0 = bx * 64 + tc;
   if (o < rows && i0 < cols) {
     const int64_t e = (int64_t)o * cols + i0;
     float v[16];
@@ -275,7 +274,7 @@ __global__ __launch_bounds__(256) void dequant_bf16_kernel(QuantPlanes q, int ro
   if (!wt) return;
   __syncthreads();
   // transposed: thread -> column i = i-tile + tr, rows o0 .. o0+15
-  const int i = blockIdx.x * 64 + tr, o0 = blockIdx.y * 64 + tc;
+  const int i = bx * 64 + tr, o0 = by * 64 + tc;
   if (i < cols && o0 < rows) {
     uint32_t p[8];
 #pragma unroll
@@ -285,15 +284,33 @@ __global__ __launch_bounds__(256) void dequant_bf16_kernel(QuantPlanes q, int ro
     dst[1] = make_uint4(p[4], p[5], p[6], p[7]);
   }
 }
-int dequant_bf16(const QuantPlanes& q, int rows, int cols, uint16_t* w, uint16_t* wt, hipStream_t s) {
+// Many matrices in one launch: workgroup b decodes tile (b - first) of the matrix whose tile
+// range [first, first + tiles) holds b (binary search over the descriptor table).
+__global__ __launch_bounds__(256) void dequant_bf16_many_kernel(const DequantJob* __restrict__ jobs, int njobs) {
+  __shared__ uint16_t tile[64][66];
+  const int64_t b = blockIdx.x;
+  int lo = 0, hi = njobs - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (jobs[mid].first <= b) lo = mid; else hi = mid - 1;
+  }
+  const DequantJob j = jobs[lo];
+  const int64_t t = b - j.first;
+  const int tx = (j.cols + 63) / 64;
+  dequant_bf16_tile(j.q, j.rows, j.cols, j.w, j.wt, (int)(t % tx), (int)(t / tx), tile);
+}
+int dequant_bf16_many(const DequantJob* jobs_dev, int njobs, int64_t total_tiles, hipStream_t s) {
+  if (!njobs || !total_tiles) return SMHIP_OK;
+  SMHIP_REQUIRE(total_tiles < ((int64_t)1 << 31), "dequant_bf16_many: too many tiles");
+  hipLaunchKernelGGL(dequant_bf16_many_kernel, dim3((unsigned)total_tiles), dim3(256), 0, s, jobs_dev, njobs);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+int dequant_bf16_check(const QuantPlanes& q, int rows, int cols, const uint16_t* w, const uint16_t* wt) {
   SMHIP_REQUIRE(q.n == (int64_t)rows * cols, "dequant_bf16: shape does not match the planes");
   SMHIP_REQUIRE(rows % 16 == 0 && cols % 16 == 0, "dequant_bf16: rows and cols must be multiples of 16");
   SMHIP_REQUIRE(q.kind == SMHIP_QTYPE_Q8_0 || q.kind == SMHIP_QTYPE_Q4_K, "dequant_bf16: qtype must be Q8_0 or Q4_K");
   SMHIP_REQUIRE(((uintptr_t)w | (uintptr_t)wt) % 16 == 0, "dequant_bf16: outputs must be 16-byte aligned");
-  if (!w && !wt) return SMHIP_OK;
-  hipLaunchKernelGGL(dequant_bf16_kernel, dim3(ceil_div(cols, 64), ceil_div(rows, 64)), dim3(256), 0, s, q, rows, cols,
-                     w, wt);
-  SMHIP_CHECK_LAUNCH();
   return SMHIP_OK;
 }
 }  // namespace smhip
