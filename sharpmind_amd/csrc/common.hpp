@@ -163,6 +163,7 @@ struct GemmArgs {
   const float* R;      // optional residual: C = alpha*AB + bias + R  (fp32 output only)
   int64_t ldr;
   int prof_cat;        // live-timing category (0: by operand kind)
+  struct SkinnyBatch* defer;  // rank-sized products: queue the split reduction here (see skinny_flush)
 };
 int gemm(const GemmArgs& g, hipStream_t s);
 

@@ -82,6 +82,7 @@ struct Engine {
   // straight to LDS; without room for it the GEMMs decode the codes in their loaders
   bool base_ws = false;
   uint16_t *emb_b = nullptr, *emb_bt = nullptr;
+  SkinnyBatch skb;                // deferred split reductions of a layer's adapter gradients
   DequantJob* dq_jobs = nullptr;  // device table of the per-step decode (one launch)
   int dq_njobs = 0;
   int64_t dq_tiles = 0;
@@ -272,6 +273,10 @@ static int build(Engine* e) {
       const int h_cols[5] = {0, e->qd, e->qd + e->kvd, 0, F};
       SMHIP_CHECK_HIP(hipMemcpy(w.lb_cols, h_cols, sizeof(h_cols), hipMemcpyHostToDevice));
     }
+    // partials of one layer's dA / dB products (a full arena flushes early, which is only slower)
+    e->skb.cap = (size_t)96 << 20;
+    e->skb.arena = (float*)dalloc(e, e->skb.cap);
+    if (!e->skb.arena) return fail(SMHIP_ENOMEM, "engine: adapter-gradient partials");
   }
 
   // --- activations
@@ -471,14 +476,8 @@ static int proj_backward(Engine* e, int l, int p, const void* dY, const float* d
     gb.B = act_r(e, dY, Out);
     gb.C = w.lb[p].grad; gb.ldc = Out;
     gb.split_k = split_arg(e, nr, Out, T);
+    gb.defer = &e->skb;
     if (int rc = gemm(gb, s)) return rc;
-    if (e->nblk[p] > 1) {
-      if (p == P_QKV) {
-        if (int rc = lora_mask(w.lb[p].grad, nr, e->c.lora_rank, Out, w.lb_cols, 3, s)) return rc;
-      } else {
-        if (int rc = lora_mask(w.lb[p].grad, nr, e->c.lora_rank, Out, w.lb_cols + 3, 2, s)) return rc;
-      }
-    }
     // dA += s x^T z   [In, nr]
     GemmArgs ga{};
     ga.precision = prec(e); ga.alpha = sc; ga.beta = 1.f;
@@ -487,6 +486,7 @@ static int proj_backward(Engine* e, int l, int p, const void* dY, const float* d
     ga.B = act_r(e, e->z, nr);
     ga.C = w.la[p].grad; ga.ldc = nr;
     ga.split_k = split_arg(e, In, nr, T);
+    ga.defer = &e->skb;
     if (int rc = gemm(ga, s)) return rc;
     g.K2 = nr;
     g.A2 = act_k(e, e->z, nr);
@@ -631,6 +631,14 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
     R_(proj_backward(e, l, P_QKV, e->dqkv, e->bf ? nullptr : (float*)e->dqkv, sv.xn1, e->dx, 0, nullptr, s));
     R_(rmsnorm_backward(e->dx, sv.h_in, 1, sv.rinv1, w.norm1.data, w.norm1.grad, e->dh, T, d, 1,
                         e->bf ? (uint16_t*)e->dh_ta : nullptr, s));
+    if (e->lora) {
+      // the layer's adapter gradients: queued split reductions, then the off-diagonal blocks
+      // of the fused B gradients back to zero
+      R_(skinny_flush(&e->skb, s));
+      const int nrq = e->nr[P_QKV], nrg = e->nr[P_GU];
+      R_(lora_mask(w.lb[P_QKV].grad, nrq, c.lora_rank, e->Out[P_QKV], w.lb_cols, 3, s));
+      R_(lora_mask(w.lb[P_GU].grad, nrg, c.lora_rank, e->Out[P_GU], w.lb_cols + 3, 2, s));
+    }
   }
   if (!e->lora) R_(embedding_backward(e->dh, ids, e->emb.grad, T, d, V, s));  // BackpropEngine.cs:203-205
 #undef R_

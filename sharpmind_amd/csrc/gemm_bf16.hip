@@ -746,9 +746,9 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   if (g.K2 == 0 && !g.bias && !g.R && (g.N <= 64 || g.M <= 64) && (bm == SRC_BF16_K || bm == SRC_BF16_R)) {
     const int r = g.N <= 64
         ? gemm_skinny(g.M, g.N, g.K, g.A.p, g.A.ld, am == SRC_BF16_K, g.B.p, g.B.ld, bm == SRC_BF16_K, g.alpha,
-                      g.beta, g.C, g.ldc, false, g.c_bf16 != 0, s)
+                      g.beta, g.C, g.ldc, false, g.c_bf16 != 0, g.defer, s)
         : gemm_skinny(g.N, g.M, g.K, g.B.p, g.B.ld, bm == SRC_BF16_K, g.A.p, g.A.ld, am == SRC_BF16_K, g.alpha,
-                      g.beta, g.C, g.ldc, true, g.c_bf16 != 0, s);
+                      g.beta, g.C, g.ldc, true, g.c_bf16 != 0, g.defer, s);
     if (r != 0) return r;
   }
   if (am == SRC_BF16_R && bm != SRC_BF16_R) return 0;

@@ -39,9 +39,29 @@ int colsum_add(const float* dY, float* db, int B, int Out, hipStream_t s);
 
 // gemm_bf16.hip: 1 = ran, 0 = not eligible (generic kernel), <0 = error
 int gemm_bf16_fast(const GemmArgs& g, hipStream_t s);
+// Deferred split reductions of rank-sized products: gemm_skinny with a batch writes its fp32
+// partials into the batch's arena and queues the reduction; skinny_flush reduces everything
+// queued in one launch (also called by gemm_skinny when the arena or the queue is full).
+// Products whose result is not read before the flush (gradient accumulations) may be deferred.
+struct SkinnyJob {
+  const float* partial;
+  void* C;
+  int64_t ldc;
+  int S, M, n;
+  float alpha, beta;
+  int trans, c_bf16;
+};
+struct SkinnyBatch {
+  static constexpr int kMaxJobs = 8;
+  float* arena = nullptr;
+  size_t cap = 0, used = 0;  // bytes
+  int n = 0;
+  SkinnyJob job[kMaxJobs];
+};
+int skinny_flush(SkinnyBatch* b, hipStream_t s);
 int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, const void* small, int64_t lds,
                 bool small_k, float alpha, float beta, void* C, int64_t ldc, bool trans_out, bool c_bf16,
-                hipStream_t s);
+                SkinnyBatch* defer, hipStream_t s);
 
 // quant.hip
 int dequant_raw(int qtype, const void* raw, float* out, int64_t n, hipStream_t s);

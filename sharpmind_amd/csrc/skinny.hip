@@ -300,6 +300,45 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
   }
 }
 
+// The queued reductions of a SkinnyBatch in one launch: thread q takes float4 q of the
+// concatenated outputs; the same fixed-order sum as skinny_reduce_kernel.
+struct BatchArgs {
+  int n;
+  SkinnyJob job[SkinnyBatch::kMaxJobs];
+  int64_t first4[SkinnyBatch::kMaxJobs + 1];  // prefix sums of M * n / 4
+};
+__global__ __launch_bounds__(256) void skinny_reduce_batch_kernel(BatchArgs b) {
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= b.first4[b.n]) return;
+  int k = 0;
+  while (g >= b.first4[k + 1]) k++;
+  const SkinnyJob& j = b.job[k];
+  const int64_t q = g - b.first4[k];
+  const int n4 = j.n / 4;
+  const int64_t m = q / n4;
+  const int r = (int)(q - m * n4) * 4;
+  const int64_t plane = (int64_t)j.M * j.n / 4;
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const f4v* p4 = reinterpret_cast<const f4v*>(j.partial) + q;
+  f4v acc = {0.f, 0.f, 0.f, 0.f};
+  for (int sidx = 0; sidx < j.S; sidx++) acc += __builtin_nontemporal_load(p4 + sidx * plane);
+  const float v[4] = {acc[0], acc[1], acc[2], acc[3]};
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const int64_t ci = j.trans ? (int64_t)(r + e) * j.ldc + m : m * j.ldc + r + e;
+    float o = j.alpha * v[e];
+    if (j.c_bf16) {
+      uint16_t* c = (uint16_t*)j.C + ci;
+      if (j.beta != 0.f) o += j.beta * bf2f(*c);
+      *c = f2bf(o);
+    } else {
+      float* c = (float*)j.C + ci;
+      if (j.beta != 0.f) o += j.beta * *c;
+      *c = o;
+    }
+  }
+}
+
 template <bool BIGK, bool SMALLK, int NB>
 static void launch(const Args& a, dim3 grid, bool trans, bool cbf, hipStream_t s) {
   if (trans) {
@@ -325,9 +364,26 @@ static void launch_nb(int nb, const Args& a, dim3 grid, bool trans, bool cbf, hi
 // Returns 1 if the skinny path ran, 0 if the operands do not fit it (caller falls back to
 // the general GEMM), < 0 on error.  big_k / small_k: operand k-contiguous.  trans_out: the
 // result (m, r) is stored at C[r * ldc + m].
+int skinny_flush(SkinnyBatch* b, hipStream_t s) {
+  using namespace sk;
+  if (!b || b->n == 0) return SMHIP_OK;
+  BatchArgs a{};
+  a.n = b->n;
+  a.first4[0] = 0;
+  for (int k = 0; k < b->n; k++) {
+    a.job[k] = b->job[k];
+    a.first4[k + 1] = a.first4[k] + (int64_t)b->job[k].M * b->job[k].n / 4;
+  }
+  b->n = 0;
+  b->used = 0;
+  hipLaunchKernelGGL(skinny_reduce_batch_kernel, dim3(ceil_div(a.first4[a.n], 256)), dim3(256), 0, s, a);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
 int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, const void* small, int64_t lds,
                 bool small_k, float alpha, float beta, void* C, int64_t ldc, bool trans_out, bool c_bf16,
-                hipStream_t s) {
+                SkinnyBatch* defer, hipStream_t s) {
   using namespace sk;
   if (n < 1 || n > 64 || n % 16 || M < 1 || K < BKT || K % BKT) return 0;
   if (((uintptr_t)big | (uintptr_t)small) % 16 || ldb % 8) return 0;
@@ -353,7 +409,15 @@ int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, c
   a.kps = ceil_div(nk, S);
   S = ceil_div(nk, a.kps);
   a.partial = nullptr;
-  if (S > 1) {
+  const size_t pbytes = (sizeof(float) * (size_t)S * M * n + 255) & ~(size_t)255;
+  const bool deferred = S > 1 && defer && pbytes <= defer->cap;
+  if (deferred) {
+    if (defer->n == SkinnyBatch::kMaxJobs || defer->used + pbytes > defer->cap)
+      if (int rc = skinny_flush(defer, s)) return rc;
+    a.partial = (float*)((char*)defer->arena + defer->used);
+    defer->job[defer->n++] = SkinnyJob{a.partial, C, ldc, S, M, n, alpha, beta, trans_out ? 1 : 0, c_bf16 ? 1 : 0};
+    defer->used += pbytes;
+  } else if (S > 1) {
     a.partial = (float*)workspace(s, sizeof(float) * (size_t)S * M * n, 7);
     if (!a.partial) return fail(SMHIP_ENOMEM, "gemm_skinny: split workspace");
   }
@@ -365,7 +429,7 @@ int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, c
   else launch_nb<false, false>(n / 16, a, grid, trans_out, c_bf16, s);
   SMHIP_CHECK_LAUNCH();
   prof_add(PROF_GEMM, ev0, prof_mark(s), 2.0 * M * n * (double)K, M, n, K);
-  if (S > 1) {
+  if (S > 1 && !deferred) {
     const int blocks = ceil_div((int64_t)M * n / 4, 256);
     if (trans_out) {
       if (c_bf16) hipLaunchKernelGGL((skinny_reduce_kernel<true, true>), dim3(blocks), dim3(256), 0, s, a.partial, S, M, n, C, ldc, alpha, beta);
