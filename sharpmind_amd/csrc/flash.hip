@@ -57,18 +57,18 @@ __device__ inline bf16x8 tload(const uint16_t* row, int c16, int lane) {
 }
 
 // Stage rows [r0, r0+NR) x D of a bf16 matrix into LDS as [NR][D+8] and/or transposed [D][NR+8].
-template <int D, int NR, bool ROWS, bool TRANS>
+template <int D, int NR, bool ROWS, bool TRANS, int NT = 256>
 __device__ inline void stage(const uint16_t* __restrict__ g, int64_t ld, int r0, uint16_t* sRow,
                              uint16_t* sT) {
   constexpr int RP = D + 8, TP = NR + 4;
   if constexpr (ROWS) {
-    for (int c = threadIdx.x; c < NR * D / 8; c += 256) {
+    for (int c = threadIdx.x; c < NR * D / 8; c += NT) {
       const int r = c / (D / 8), dc = (c % (D / 8)) * 8;
       *reinterpret_cast<uint4*>(sRow + r * RP + dc) = *reinterpret_cast<const uint4*>(g + (int64_t)(r0 + r) * ld + dc);
     }
   }
   if constexpr (TRANS) {
-    for (int c = threadIdx.x; c < (NR / 2) * (D / 8); c += 256) {
+    for (int c = threadIdx.x; c < (NR / 2) * (D / 8); c += NT) {
       const int rp = c % (NR / 2), dc = (c / (NR / 2)) * 8;
       uint4 a = *reinterpret_cast<const uint4*>(g + (int64_t)(r0 + 2 * rp) * ld + dc);
       uint4 b = *reinterpret_cast<const uint4*>(g + (int64_t)(r0 + 2 * rp + 1) * ld + dc);
@@ -87,15 +87,15 @@ __device__ inline void stage(const uint16_t* __restrict__ g, int64_t ld, int r0,
 // of rows per 16-byte column chunk) into registers, store() writes them to LDS as [NR][D+8]
 // and/or transposed [D][NR+8].  Loading tile t+1 before the MFMAs of tile t hides the
 // global latency behind the compute.
-template <int D, int NR>
+template <int D, int NR, int NT = 256>
 struct Pref {
   static constexpr int U = (NR / 2) * (D / 8);  // (row pair, chunk) units
-  static constexpr int PER = (U + 255) / 256;
+  static constexpr int PER = (U + NT - 1) / NT;
   static_assert(PER <= 2, "Pref holds at most two units per thread");
   uint4 a0, b0, a1, b1;  // named registers: no dynamically indexed (scratch) arrays
-  // unit c's two rows; units past U (only when U is not a multiple of 256) read row pair 0
+  // unit c's two rows; units past U (only when U is not a multiple of NT) read row pair 0
   __device__ static inline uint4 ld1(const uint16_t* __restrict__ g, int64_t ld, int r0, int c, int odd) {
-    if constexpr (U % 256 != 0) c = c < U ? c : 0;
+    if constexpr (U % NT != 0) c = c < U ? c : 0;
     const int rp = c % (NR / 2), dc = (c / (NR / 2)) * 8;
     return *reinterpret_cast<const uint4*>(g + (int64_t)(r0 + 2 * rp + odd) * ld + dc);
   }
@@ -103,8 +103,8 @@ struct Pref {
     a0 = ld1(g, ld, r0, threadIdx.x, 0);
     b0 = ld1(g, ld, r0, threadIdx.x, 1);
     if constexpr (PER > 1) {
-      a1 = ld1(g, ld, r0, 256 + threadIdx.x, 0);
-      b1 = ld1(g, ld, r0, 256 + threadIdx.x, 1);
+      a1 = ld1(g, ld, r0, NT + threadIdx.x, 0);
+      b1 = ld1(g, ld, r0, NT + threadIdx.x, 1);
     }
   }
   template <bool ROWS, bool TRANS>
@@ -129,24 +129,31 @@ struct Pref {
   template <bool ROWS, bool TRANS>
   __device__ inline void store(uint16_t* sRow, uint16_t* sT) const {
     store1<ROWS, TRANS>(sRow, sT, threadIdx.x, a0, b0);
-    if constexpr (PER > 1) store1<ROWS, TRANS>(sRow, sT, 256 + threadIdx.x, a1, b1);
+    if constexpr (PER > 1) store1<ROWS, TRANS>(sRow, sT, NT + threadIdx.x, a1, b1);
   }
 };
 
 // ============================================================================
-// forward: grid (S/128, Hq, B), 4 waves x 32 queries, key tiles of 64
+// forward: grid (S/128, Hq, B), 4 waves x 32 queries, key tiles of 64.
+// PAIR (S/128 even): grid (S/256, Hq, B) of 8 waves; waves 0-3 take query block nb-1-x and
+// waves 4-7 block x, so every workgroup (and every SIMD, which hosts wave s and wave s+4)
+// carries the same causal work and the two blocks share the staged K/V tiles.  Without it
+// the query-block index, the fastest grid dimension, lands each block on one XCD (blocks
+// are dispatched round-robin over the 8 XCDs): the XCD of the longest rows bounded the kernel.
 // ============================================================================
-template <int D>
-__global__ __launch_bounds__(256) void fa_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+template <int D, bool PAIR>
+__global__ __launch_bounds__(PAIR ? 512 : 256) void fa_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                      const uint16_t* __restrict__ v, uint16_t* __restrict__ o,
                                                      float* __restrict__ lse, int S, int Hq, int Hkv, int64_t ldq,
                                                      int64_t ldk, int64_t ldv, int64_t ldo, float sl2) {
-  constexpr int KB = 64, KP = D + 8, VP = KB + 4;
+  constexpr int KB = 64, KP = D + 8, VP = KB + 4, NT = PAIR ? 512 : 256;
   __shared__ __attribute__((aligned(16))) uint16_t sK[KB * KP];
   __shared__ __attribute__((aligned(16))) uint16_t sVt[D * VP];
-  const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;  // longest causal rows first
+  const int nb = PAIR ? 2 * (int)gridDim.x : (int)gridDim.x;
+  const int half = PAIR ? (int)(threadIdx.x >> 8) : 0;
+  const int qb = half == 0 ? nb - 1 - (int)blockIdx.x : (int)blockIdx.x;  // longest causal rows first
   const int h = blockIdx.y, b = blockIdx.z, kvh = h / (Hq / Hkv);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = (threadIdx.x >> 6) & 3;
   const int qi = qb * 128 + w * 32 + (lane & 31);
   const uint16_t* kb = k + (int64_t)b * S * ldk + kvh * D;
   const uint16_t* vb = v + (int64_t)b * S * ldv + kvh * D;
@@ -161,13 +168,13 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(const uint16_t* __restrict_
 #pragma unroll
   for (int i = 0; i < D / 32; i++) zero16(oacc[i]);
   float m = -INFINITY, l = 0.f;
-  const int kend = (qb + 1) * 128;
+  const int kend = (nb - (int)blockIdx.x) * 128;  // the longer block of the workgroup
   const int wq_last = qb * 128 + w * 32 + 31;  // last query of this wave
 
   for (int k0 = 0; k0 < kend; k0 += KB) {
     __syncthreads();
-    stage<D, KB, true, false>(kb, ldk, k0, sK, nullptr);
-    stage<D, KB, false, true>(vb, ldv, k0, nullptr, sVt);
+    stage<D, KB, true, false, NT>(kb, ldk, k0, sK, nullptr);
+    stage<D, KB, false, true, NT>(vb, ldv, k0, nullptr, sVt);
     __syncthreads();
     if (k0 > wq_last) continue;  // whole tile masked for this wave
     floatx16 sacc[2];
@@ -261,22 +268,25 @@ __global__ __launch_bounds__(256) void fa_bwd_pre_kernel(const uint16_t* __restr
 // 32-query MFMA blocks per wave per tile).  Writes per-query-head partials dKh/dVh
 // [B, S, Hq, D] fp32.
 // ============================================================================
-template <int D>
-__global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
+template <int D, bool PAIR>
+__global__ __launch_bounds__(PAIR ? 512 : 256) void fa_bwd_dkdv_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
     float* __restrict__ dKh, float* __restrict__ dVh, int S, int Hq, int Hkv, int64_t ldq, int64_t ldk,
     int64_t ldv, int64_t lddo, float sl2, float scale) {
-  constexpr int QB = 64, NQ = QB / 32, RP = D + 8, TP = QB + 4;
+  constexpr int QB = 64, NQ = QB / 32, RP = D + 8, TP = QB + 4, NT = PAIR ? 512 : 256;
   __shared__ __attribute__((aligned(16))) uint16_t sQ[QB * RP];
   __shared__ __attribute__((aligned(16))) uint16_t sQt[D * TP];
   __shared__ __attribute__((aligned(16))) uint16_t sdO[QB * RP];
   __shared__ __attribute__((aligned(16))) uint16_t sdOt[D * TP];
   __shared__ __attribute__((aligned(16))) float sL[QB];
   __shared__ __attribute__((aligned(16))) float sDi[QB];
-  const int kbk = blockIdx.x;  // key block of 128
+  // key block of 128; PAIR: waves 0-3 take key block x (the most queries), waves 4-7 block nb-1-x
+  const int nb = PAIR ? 2 * (int)gridDim.x : (int)gridDim.x;
+  const int half = PAIR ? (int)(threadIdx.x >> 8) : 0;
+  const int kbk = half == 0 ? (int)blockIdx.x : nb - 1 - (int)blockIdx.x;
   const int h = blockIdx.y, b = blockIdx.z, kvh = h / (Hq / Hkv);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = (threadIdx.x >> 6) & 3;
   const int kw0 = kbk * 128 + w * 32;
   const int kj = kw0 + (lane & 31);  // this lane's key (B-operand column)
 
@@ -298,9 +308,9 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
   const float* lrow = lse + ((int64_t)b * Hq + h) * S;
   const float* drow = Di + ((int64_t)b * Hq + h) * S;
 
-  Pref<D, QB> pq, pd;
+  Pref<D, QB, NT> pq, pd;
   float pl = 0.f, pdi = 0.f;
-  const int qstart = kbk * 128;
+  const int qstart = (int)blockIdx.x * 128;  // the earlier key block of the workgroup
   pq.load(qb_, ldq, qstart);
   pd.load(db_, lddo, qstart);
   if (threadIdx.x < QB) { pl = lrow[qstart + threadIdx.x]; pdi = drow[qstart + threadIdx.x]; }
@@ -374,19 +384,21 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(
 // ============================================================================
 // backward dQ: grid (S/128, Hq, B); 4 waves x 32 queries; key tiles of 64
 // ============================================================================
-template <int D>
-__global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
+template <int D, bool PAIR>
+__global__ __launch_bounds__(PAIR ? 512 : 256) void fa_bwd_dq_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
     float* __restrict__ dq, int S, int Hq, int Hkv, int64_t ldq, int64_t ldk, int64_t ldv, int64_t lddo,
     int64_t lddq, float sl2, float scale) {
-  constexpr int KB = 64, RP = D + 8, TP = KB + 4;
+  constexpr int KB = 64, RP = D + 8, TP = KB + 4, NT = PAIR ? 512 : 256;
   __shared__ __attribute__((aligned(16))) uint16_t sK[KB * RP];
   __shared__ __attribute__((aligned(16))) uint16_t sKt[D * TP];
   __shared__ __attribute__((aligned(16))) uint16_t sV[KB * RP];
-  const int qb = (int)gridDim.x - 1 - (int)blockIdx.x;
+  const int nb = PAIR ? 2 * (int)gridDim.x : (int)gridDim.x;
+  const int half = PAIR ? (int)(threadIdx.x >> 8) : 0;
+  const int qb = half == 0 ? nb - 1 - (int)blockIdx.x : (int)blockIdx.x;
   const int h = blockIdx.y, b = blockIdx.z, kvh = h / (Hq / Hkv);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = (threadIdx.x >> 6) & 3;
   const int qi = qb * 128 + w * 32 + (lane & 31);
   bf16x8 qf[D / 16], of[D / 16];
   {
@@ -405,9 +417,9 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(
   for (int i = 0; i < D / 32; i++) zero16(acc[i]);
   const uint16_t* kb = k + (int64_t)b * S * ldk + kvh * D;
   const uint16_t* vb = v + (int64_t)b * S * ldv + kvh * D;
-  const int kend = (qb + 1) * 128;
+  const int kend = (nb - (int)blockIdx.x) * 128;  // the longer block of the workgroup
   const int wq_last = qb * 128 + w * 32 + 31;
-  Pref<D, KB> pk, pv;
+  Pref<D, KB, NT> pk, pv;
   pk.load(kb, ldk, 0);
   pv.load(vb, ldv, 0);
   for (int k0 = 0; k0 < kend; k0 += KB) {
@@ -490,11 +502,15 @@ int flash_forward(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint1
   SMHIP_REQUIRE(S % 128 == 0, "flash attention: S must be a multiple of 128");
   SMHIP_REQUIRE(Hkv > 0 && Hq % Hkv == 0, "flash attention: Hq must be a multiple of Hkv");
   const float sl2 = kLog2e / sqrtf((float)D);
-  dim3 grid(S / 128, Hq, B);
+  // pair the causal blocks (balanced workgroups) whenever their count is even
+  const bool pair = (S / 128) % 2 == 0;
+  const dim3 grid(pair ? S / 256 : S / 128, Hq, B), block(pair ? 512 : 256);
   const int ev0 = prof_mark(s);
-  if (D == 128) hipLaunchKernelGGL(fa_fwd_kernel<128>, grid, dim3(256), 0, s, q, k, v, o, lse, S, Hq, Hkv, ldq, ldk, ldv, ldo, sl2);
-  else if (D == 64) hipLaunchKernelGGL(fa_fwd_kernel<64>, grid, dim3(256), 0, s, q, k, v, o, lse, S, Hq, Hkv, ldq, ldk, ldv, ldo, sl2);
+#define FA_FWD(DD, PP) hipLaunchKernelGGL((fa_fwd_kernel<DD, PP>), grid, block, 0, s, q, k, v, o, lse, S, Hq, Hkv, ldq, ldk, ldv, ldo, sl2)
+  if (D == 128) { if (pair) FA_FWD(128, true); else FA_FWD(128, false); }
+  else if (D == 64) { if (pair) FA_FWD(64, true); else FA_FWD(64, false); }
   else return fail(SMHIP_EUNSUPPORTED, "flash attention: head_dim must be 64 or 128");
+#undef FA_FWD
   SMHIP_CHECK_LAUNCH();
   // causal: QK^T and PV over the lower triangle
   prof_add(PROF_FLASH_FWD, ev0, prof_mark(s), 2.0 * B * Hq * (double)S * S * D);
@@ -518,18 +534,19 @@ int flash_backward(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
   const int64_t rows = (int64_t)B * Hq * S;
   const int gpre = (int)std::min<int64_t>((rows + 3) / 4, (int64_t)num_cus() * 8);
   const int gred = (int)std::min<int64_t>(((int64_t)B * S * Hkv * D + 255) / 256, (int64_t)num_cus() * 8);
-  dim3 grid(S / 128, Hq, B);
+  const bool pair = (S / 128) % 2 == 0;
+  const dim3 grid(pair ? S / 256 : S / 128, Hq, B), block(pair ? 512 : 256);
   const int ev0 = prof_mark(s);
-#define FA_BWD(DD)                                                                                              \
+#define FA_BWD(DD, PP)                                                                                          \
   hipLaunchKernelGGL(fa_bwd_pre_kernel<DD>, dim3(gpre), dim3(256), 0, s, o, dO, Di, B, S, Hq, ldo, lddo);      \
-  hipLaunchKernelGGL(fa_bwd_dkdv_kernel<DD>, grid, dim3(256), 0, s, q, k, v, dO, lse, Di, dKh, dVh, S, Hq, Hkv, \
-                     ldq, ldk, ldv, lddo, sl2, scale);                                                          \
-  hipLaunchKernelGGL(fa_bwd_dq_kernel<DD>, grid, dim3(256), 0, s, q, k, v, dO, lse, Di, dq, S, Hq, Hkv, ldq,   \
+  hipLaunchKernelGGL((fa_bwd_dkdv_kernel<DD, PP>), grid, block, 0, s, q, k, v, dO, lse, Di, dKh, dVh, S, Hq,   \
+                     Hkv, ldq, ldk, ldv, lddo, sl2, scale);                                                     \
+  hipLaunchKernelGGL((fa_bwd_dq_kernel<DD, PP>), grid, block, 0, s, q, k, v, dO, lse, Di, dq, S, Hq, Hkv, ldq, \
                      ldk, ldv, lddo, lddq, sl2, scale);                                                         \
   hipLaunchKernelGGL(fa_group_reduce_kernel<DD>, dim3(gred), dim3(256), 0, s, dKh, dVh, dk, dv, B, S, Hq, Hkv,  \
                      lddk, lddv);
-  if (D == 128) { FA_BWD(128) }
-  else if (D == 64) { FA_BWD(64) }
+  if (D == 128) { if (pair) { FA_BWD(128, true) } else { FA_BWD(128, false) } }
+  else if (D == 64) { if (pair) { FA_BWD(64, true) } else { FA_BWD(64, false) } }
   else return fail(SMHIP_EUNSUPPORTED, "flash attention: head_dim must be 64 or 128");
 #undef FA_BWD
   SMHIP_CHECK_LAUNCH();

@@ -43,7 +43,8 @@ def _oracle(orc, q, k, v, dO, B, S, Hq, Hkv, D):
     return probs, out, dq, dk, dv
 
 
-@pytest.mark.parametrize("B,S,Hq,Hkv,D", [(2, 256, 4, 2, 128), (1, 384, 2, 2, 64), (1, 128, 8, 1, 128)])
+@pytest.mark.parametrize("B,S,Hq,Hkv,D", [(2, 256, 4, 2, 128), (1, 384, 2, 2, 64), (1, 128, 8, 1, 128), (1, 1024, 4, 2, 128),
+                                         (1, 512, 2, 1, 64)])
 def test_flash_forward_backward(orc, dev, B, S, Hq, Hkv, D):
     rng = np.random.default_rng(S + D + Hq)
     q = _bf16_round(rng.standard_normal((B, S, Hq, D)).astype(np.float32))
