@@ -247,8 +247,8 @@ int smhip_gguf_tensor_info(const char* path, int64_t index, char* name, int64_t 
                            int64_t* dims, int64_t* file_offset);
 /* Diagnostics: copy a saved activation of the last forward to host memory.  what: "h_in", "h_mid",
  * "xn1", "qkv", "q", "k", "v", "o", "gu", "act" (of `layer`), "h_fin", "logits" ("logits" holds
- * dLogits after a fp32-mode backward).  Element type is bf16 for "xn1|q|k|v|o|gu|act" in bf16
- * mode, fp32 otherwise. */
+ * dLogits after a fp32-mode backward).  Element type is bf16 for "xn1|q|k|v|o|gu|act" (and "qkv" with
+ * head_dim 64 or 128) in bf16 mode, fp32 otherwise. */
 int smhip_engine_read_activation(void* engine, const char* what, int layer, void* host, int64_t nbytes);
 /* Live kernel timing on the calling thread: between begin and end, the GEMM and flash-attention
  * launchers bracket their kernels with HIP events on the launch stream.  end synchronises and writes

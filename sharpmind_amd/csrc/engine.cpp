@@ -57,7 +57,8 @@ struct LayerW {
 };
 
 struct Saved {
-  float *h_in, *rinv1, *qkv, *rinv_qk, *lse, *probs, *h_mid, *rinv2;
+  float *h_in, *rinv1, *rinv_qk, *lse, *probs, *h_mid, *rinv2;
+  void *qkv;  // q|k|v projection output: bf16 when Engine::qkv_bf, fp32 otherwise
   void *xn1, *q, *k, *v, *o, *xn2, *gu, *act;
   void* u[4];  // LoRA x.A per projection
 };
@@ -66,6 +67,7 @@ struct Engine {
   smhip_model_config c;
   int T, qd, kvd, nqkv, In[4], Out[4], nr[4], nblk[4];
   bool bf, lora;
+  bool qkv_bf;  // bf16 engines with head_dim 64 / 128 keep the q|k|v projection output in bf16
   size_t esz;  // activation element size
   // arenas
   float* train = nullptr; float* grad = nullptr; float* m = nullptr; float* v = nullptr;
@@ -93,7 +95,8 @@ struct Engine {
   float *h_fin, *rinv_f, *logits, *cosT, *sinT, *loss, *gnorm;
   void *xnf, *dlogits;
   // backward work
-  float *dh, *dx, *dact, *dq, *dk, *dv;
+  float *dh, *dx, *dq, *dk, *dv;
+  void* dact;  // dL/d(SwiGLU output): bf16 in bf16 engines
   void *dh_ta, *dgu, *dO, *dqkv, *z;
   void* flash_ws = nullptr;
   int step = 0;
@@ -123,6 +126,7 @@ static int build(Engine* e) {
   e->bf = c.precision == SMHIP_PREC_BF16;
   e->lora = c.lora_rank > 0;
   e->esz = e->bf ? 2 : 4;
+  e->qkv_bf = e->bf && (c.head_dim == 64 || c.head_dim == 128);
   const int d = c.d_model, F = c.ffn_dim, V = c.vocab, r = c.lora_rank;
   e->In[P_QKV] = d; e->Out[P_QKV] = e->nqkv; e->nr[P_QKV] = 3 * r; e->nblk[P_QKV] = 3;
   e->In[P_O] = e->qd; e->Out[P_O] = d; e->nr[P_O] = r; e->nblk[P_O] = 1;
@@ -289,7 +293,7 @@ static int build(Engine* e) {
     s.h_in = (float*)dalloc(e, sizeof(float) * (size_t)T * d);
     s.rinv1 = (float*)dalloc(e, sizeof(float) * T);
     s.xn1 = dalloc(e, ES * (size_t)T * d);
-    s.qkv = (float*)dalloc(e, sizeof(float) * (size_t)T * e->nqkv);
+    s.qkv = dalloc(e, (e->qkv_bf ? 2 : 4) * (size_t)T * e->nqkv);
     s.rinv_qk = (float*)dalloc(e, sizeof(float) * (size_t)T * (c.n_heads + c.n_kv_heads));
     s.q = dalloc(e, ES * (size_t)T * e->qd);
     s.k = dalloc(e, ES * (size_t)T * e->kvd);
@@ -318,7 +322,7 @@ static int build(Engine* e) {
   const int wmax = std::max(std::max(d, F), std::max(e->nqkv, 2 * F));
   e->dh = (float*)dalloc(e, sizeof(float) * (size_t)T * d);
   e->dx = (float*)dalloc(e, sizeof(float) * (size_t)T * d);
-  e->dact = (float*)dalloc(e, sizeof(float) * (size_t)T * F);
+  e->dact = dalloc(e, ES * (size_t)T * F);
   e->dq = (float*)dalloc(e, sizeof(float) * (size_t)T * e->qd);
   e->dk = (float*)dalloc(e, sizeof(float) * (size_t)T * e->kvd);
   e->dv = (float*)dalloc(e, sizeof(float) * (size_t)T * e->kvd);
@@ -541,8 +545,8 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
     float* h_out = (l + 1 < c.n_layers) ? e->sv[l + 1].h_in : e->h_fin;
     R_(rmsnorm_forward(sv.h_in, w.norm1.data, e->bf ? nullptr : (float*)sv.xn1, e->bf ? (uint16_t*)sv.xn1 : nullptr,
                        sv.rinv1, T, d, c.norm_eps, s));
-    R_(proj_forward(e, l, P_QKV, sv.xn1, sv.qkv, 0, nullptr, s));
-    R_(qkv_prep_forward(sv.qkv, sv.q, sv.k, sv.v, sv.rinv_qk, c.qk_norm ? w.qn.data : nullptr,
+    R_(proj_forward(e, l, P_QKV, sv.xn1, sv.qkv, e->qkv_bf, nullptr, s));
+    R_(qkv_prep_forward(sv.qkv, e->qkv_bf, sv.q, sv.k, sv.v, sv.rinv_qk, c.qk_norm ? w.qn.data : nullptr,
                         c.qk_norm ? w.kn.data : nullptr, e->cosT, e->sinT, T, c.seq, Hq, Hkv, D, c.qk_norm,
                         c.rope_neox, c.norm_eps, e->bf, s));
     if (e->bf) {
@@ -608,7 +612,8 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
     Saved& sv = e->sv[l];
     LayerW& w = e->L[l];
     // FfnBackward (BackpropEngine.cs:623-657)
-    R_(proj_backward(e, l, P_D, e->dh_ta, e->dh, sv.act, e->dact, 0, nullptr, s));
+    if (e->bf) R_(proj_backward(e, l, P_D, e->dh_ta, e->dh, sv.act, nullptr, 1, e->dact, s));
+    else R_(proj_backward(e, l, P_D, e->dh_ta, e->dh, sv.act, (float*)e->dact, 0, nullptr, s));
     R_(swiglu_fused_backward(e->dact, sv.gu, e->dgu, T, F, e->bf, s));
     R_(proj_backward(e, l, P_GU, e->dgu, e->bf ? nullptr : (float*)e->dgu, sv.xn2, e->dx, 0, nullptr, s));
     // norm2 backward, residual add into dh (BackpropEngine.cs:521-526)
@@ -624,7 +629,7 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
       R_(attention_probs_backward((const float*)e->dO, (const float*)sv.q, (const float*)sv.k, (const float*)sv.v,
                                   sv.probs, e->dq, e->dk, e->dv, c.batch, c.seq, Hq, Hkv, D, s));
     }
-    R_(qkv_prep_backward(e->dq, e->dk, e->dv, sv.qkv, sv.rinv_qk, c.qk_norm ? w.qn.data : nullptr,
+    R_(qkv_prep_backward(e->dq, e->dk, e->dv, sv.qkv, e->qkv_bf, sv.rinv_qk, c.qk_norm ? w.qn.data : nullptr,
                          c.qk_norm ? w.kn.data : nullptr, c.qk_norm ? w.qn.grad : nullptr,
                          c.qk_norm ? w.kn.grad : nullptr, e->cosT, e->sinT, e->dqkv, T, c.seq, Hq, Hkv, D,
                          c.qk_norm, c.rope_neox, e->bf, s));
@@ -1323,7 +1328,7 @@ int smhip_engine_read_activation(void* engine, const char* what, int layer, void
   if (w == "h_in") { src = s.h_in; bytes = T * d * 4; }
   else if (w == "h_mid") { src = s.h_mid; bytes = T * d * 4; }
   else if (w == "xn1") { src = s.xn1; bytes = T * d * es; }
-  else if (w == "qkv") { src = s.qkv; bytes = T * e->nqkv * 4; }
+  else if (w == "qkv") { src = s.qkv; bytes = T * e->nqkv * (e->qkv_bf ? 2 : 4); }
   else if (w == "q") { src = s.q; bytes = T * e->qd * es; }
   else if (w == "k") { src = s.k; bytes = T * e->kvd * es; }
   else if (w == "v") { src = s.v; bytes = T * e->kvd * es; }

@@ -177,6 +177,22 @@ template <int E> __device__ __forceinline__ void ldE(const float* p, float* v) {
 #pragma unroll
   for (int i = 0; i < E; i++) v[i] = f[i];
 }
+// E bf16 values (4 or 8 bytes) widened to fp32
+template <int E> __device__ __forceinline__ void ldE(const uint16_t* p, float* v) {
+  uint32_t w[E / 2];
+  if constexpr (E == 4) {
+    const uint2 t = *reinterpret_cast<const uint2*>(p);
+    w[0] = t.x;
+    w[1] = t.y;
+  } else {
+    w[0] = *reinterpret_cast<const uint32_t*>(p);
+  }
+#pragma unroll
+  for (int i = 0; i < E / 2; i++) {
+    v[2 * i] = __builtin_bit_cast(float, w[i] << 16);
+    v[2 * i + 1] = __builtin_bit_cast(float, w[i] & 0xFFFF0000u);
+  }
+}
 template <int E, typename TA> __device__ __forceinline__ void stE(TA* p, const float* v) {
   if constexpr (sizeof(TA) == 4) {
     typename VecF<E>::T t;
@@ -198,9 +214,9 @@ __device__ __forceinline__ float half_sum(float v) {
   return v;
 }
 
-template <int D, typename TA>
+template <int D, typename TA, typename TQ>
 __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
-    const float* __restrict__ qkv, TA* __restrict__ qo, TA* __restrict__ ko, TA* __restrict__ vo,
+    const TQ* __restrict__ qkv, TA* __restrict__ qo, TA* __restrict__ ko, TA* __restrict__ vo,
     float* __restrict__ rinv, const float* __restrict__ wq, const float* __restrict__ wk,
     const float* __restrict__ cosT, const float* __restrict__ sinT, int T, int S, int Hq, int Hkv,
     int qk_norm, int neox, float eps) {
@@ -215,7 +231,7 @@ __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
     const bool live = r < rows;
     const int64_t rr = live ? r : rows - 1;
     const int t = (int)(rr / H), hh = (int)(rr % H);
-    const float* x = qkv + (int64_t)t * nqkv + hh * D + l * E;
+    const TQ* x = qkv + (int64_t)t * nqkv + hh * D + l * E;
     float v[E];
     ldE<E>(x, v);
     if (hh >= Hq + Hkv) {
@@ -259,10 +275,10 @@ __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
   }
 }
 
-template <int D, typename TA>
+template <int D, typename TA, typename TQ>
 __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
     const float* __restrict__ dq, const float* __restrict__ dk, const float* __restrict__ dv,
-    const float* __restrict__ qkv, const float* __restrict__ rinv, const float* __restrict__ wq,
+    const TQ* __restrict__ qkv, const float* __restrict__ rinv, const float* __restrict__ wq,
     const float* __restrict__ wk, const float* __restrict__ cosT, const float* __restrict__ sinT,
     TA* __restrict__ dqkv, float* __restrict__ part, int T, int S, int Hq, int Hkv, int qk_norm, int neox) {
   constexpr int E = D / 32, P = D / 2;
@@ -345,31 +361,36 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
   }
 }
 
-int qkv_prep_forward(const float* qkv, void* q, void* k, void* v, float* rinv, const float* wq,
+int qkv_prep_forward(const void* qkv, int qkv_bf16, void* q, void* k, void* v, float* rinv, const float* wq,
                      const float* wk, const float* cosT, const float* sinT, int T, int S, int Hq, int Hkv,
                      int D, int qk_norm, int neox, float eps, int bf16, hipStream_t s) {
   SMHIP_REQUIRE(D <= 128 && D % 2 == 0, "qkv prep: head_dim must be even and <= 128");
   const int64_t rows = (int64_t)T * (Hq + 2 * Hkv);
   if (D == 128 || D == 64) {
     const int gv = gridn(rows, 8);
-#define SMHIP_QKV_FWD(DD, TT) \
-  hipLaunchKernelGGL((qkv_prep_fwd_vec_kernel<DD, TT>), dim3(gv), dim3(256), 0, s, qkv, (TT*)q, (TT*)k, (TT*)v, rinv, wq, wk, cosT, sinT, T, S, Hq, Hkv, qk_norm, neox, eps)
-    if (D == 128) { if (bf16) SMHIP_QKV_FWD(128, uint16_t); else SMHIP_QKV_FWD(128, float); }
-    else { if (bf16) SMHIP_QKV_FWD(64, uint16_t); else SMHIP_QKV_FWD(64, float); }
+#define SMHIP_QKV_FWD(DD, TT, TQ) \
+  hipLaunchKernelGGL((qkv_prep_fwd_vec_kernel<DD, TT, TQ>), dim3(gv), dim3(256), 0, s, (const TQ*)qkv, (TT*)q, (TT*)k, (TT*)v, rinv, wq, wk, cosT, sinT, T, S, Hq, Hkv, qk_norm, neox, eps)
+    if (qkv_bf16) {
+      SMHIP_REQUIRE(bf16, "qkv prep: bf16 projections need bf16 outputs");
+      if (D == 128) SMHIP_QKV_FWD(128, uint16_t, uint16_t); else SMHIP_QKV_FWD(64, uint16_t, uint16_t);
+    } else if (D == 128) { if (bf16) SMHIP_QKV_FWD(128, uint16_t, float); else SMHIP_QKV_FWD(128, float, float); }
+    else { if (bf16) SMHIP_QKV_FWD(64, uint16_t, float); else SMHIP_QKV_FWD(64, float, float); }
 #undef SMHIP_QKV_FWD
     SMHIP_CHECK_LAUNCH();
     return SMHIP_OK;
   }
+  SMHIP_REQUIRE(!qkv_bf16, "qkv prep: bf16 projections need head_dim 64 or 128");
   const int g = gridn(rows, 4);
   if (bf16)
-    hipLaunchKernelGGL(qkv_prep_fwd_kernel<uint16_t>, dim3(g), dim3(256), 0, s, qkv, (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, rinv, wq, wk, cosT, sinT, T, S, Hq, Hkv, D, qk_norm, neox, eps);
+    hipLaunchKernelGGL(qkv_prep_fwd_kernel<uint16_t>, dim3(g), dim3(256), 0, s, (const float*)qkv, (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, rinv, wq, wk, cosT, sinT, T, S, Hq, Hkv, D, qk_norm, neox, eps);
   else
-    hipLaunchKernelGGL(qkv_prep_fwd_kernel<float>, dim3(g), dim3(256), 0, s, qkv, (float*)q, (float*)k, (float*)v, rinv, wq, wk, cosT, sinT, T, S, Hq, Hkv, D, qk_norm, neox, eps);
+    hipLaunchKernelGGL(qkv_prep_fwd_kernel<float>, dim3(g), dim3(256), 0, s, (const float*)qkv, (float*)q, (float*)k, (float*)v, rinv, wq, wk, cosT, sinT, T, S, Hq, Hkv, D, qk_norm, neox, eps);
   SMHIP_CHECK_LAUNCH();
   return SMHIP_OK;
 }
 
-int qkv_prep_backward(const float* dq, const float* dk, const float* dv, const float* qkv, const float* rinv,
+int qkv_prep_backward(const float* dq, const float* dk, const float* dv, const void* qkv, int qkv_bf16,
+                      const float* rinv,
                       const float* wq, const float* wk, float* dwq, float* dwk, const float* cosT,
                       const float* sinT, void* dqkv, int T, int S, int Hq, int Hkv, int D, int qk_norm,
                       int neox, int bf16, hipStream_t s) {
@@ -384,16 +405,19 @@ int qkv_prep_backward(const float* dq, const float* dk, const float* dv, const f
     part = (float*)workspace(s, sizeof(float) * (size_t)g * 2 * D, 7);
     if (!part) return fail(SMHIP_ENOMEM, "qkv prep backward: workspace");
   }
+  SMHIP_REQUIRE(vec || !qkv_bf16, "qkv prep: bf16 projections need head_dim 64 or 128");
+  SMHIP_REQUIRE(bf16 || !qkv_bf16, "qkv prep: bf16 projections need bf16 outputs");
   if (vec) {
-#define SMHIP_QKV_BWD(DD, TT) \
-  hipLaunchKernelGGL((qkv_prep_bwd_vec_kernel<DD, TT>), dim3(g), dim3(256), 0, s, dq, dk, dv, qkv, rinv, wq, wk, cosT, sinT, (TT*)dqkv, part, T, S, Hq, Hkv, qk_norm, neox)
-    if (D == 128) { if (bf16) SMHIP_QKV_BWD(128, uint16_t); else SMHIP_QKV_BWD(128, float); }
-    else { if (bf16) SMHIP_QKV_BWD(64, uint16_t); else SMHIP_QKV_BWD(64, float); }
+#define SMHIP_QKV_BWD(DD, TT, TQ) \
+  hipLaunchKernelGGL((qkv_prep_bwd_vec_kernel<DD, TT, TQ>), dim3(g), dim3(256), 0, s, dq, dk, dv, (const TQ*)qkv, rinv, wq, wk, cosT, sinT, (TT*)dqkv, part, T, S, Hq, Hkv, qk_norm, neox)
+    if (qkv_bf16) { if (D == 128) SMHIP_QKV_BWD(128, uint16_t, uint16_t); else SMHIP_QKV_BWD(64, uint16_t, uint16_t); }
+    else if (D == 128) { if (bf16) SMHIP_QKV_BWD(128, uint16_t, float); else SMHIP_QKV_BWD(128, float, float); }
+    else { if (bf16) SMHIP_QKV_BWD(64, uint16_t, float); else SMHIP_QKV_BWD(64, float, float); }
 #undef SMHIP_QKV_BWD
   } else if (bf16)
-    hipLaunchKernelGGL(qkv_prep_bwd_kernel<uint16_t>, dim3(g), dim3(256), 0, s, dq, dk, dv, qkv, rinv, wq, wk, cosT, sinT, (uint16_t*)dqkv, part, T, S, Hq, Hkv, D, qk_norm, neox);
+    hipLaunchKernelGGL(qkv_prep_bwd_kernel<uint16_t>, dim3(g), dim3(256), 0, s, dq, dk, dv, (const float*)qkv, rinv, wq, wk, cosT, sinT, (uint16_t*)dqkv, part, T, S, Hq, Hkv, D, qk_norm, neox);
   else
-    hipLaunchKernelGGL(qkv_prep_bwd_kernel<float>, dim3(g), dim3(256), 0, s, dq, dk, dv, qkv, rinv, wq, wk, cosT, sinT, (float*)dqkv, part, T, S, Hq, Hkv, D, qk_norm, neox);
+    hipLaunchKernelGGL(qkv_prep_bwd_kernel<float>, dim3(g), dim3(256), 0, s, dq, dk, dv, (const float*)qkv, rinv, wq, wk, cosT, sinT, (float*)dqkv, part, T, S, Hq, Hkv, D, qk_norm, neox);
   SMHIP_CHECK_LAUNCH();
   if (part) {
     hipLaunchKernelGGL(colsum_add2_kernel, dim3(ceil_div(2 * D, 256)), dim3(256), 0, s, part, dwq, dwk, g, D);
@@ -414,13 +438,13 @@ __global__ __launch_bounds__(256) void swiglu_fused_fwd_kernel(const TI* __restr
     st(act + i, (g / (1.f + expf(-g))) * u);
   }
 }
-template <typename TI, typename TO>
-__global__ __launch_bounds__(256) void swiglu_fused_bwd_kernel(const float* __restrict__ dA, const TI* __restrict__ gu,
+template <typename TD, typename TI, typename TO>
+__global__ __launch_bounds__(256) void swiglu_fused_bwd_kernel(const TD* __restrict__ dA, const TI* __restrict__ gu,
                                                                TO* __restrict__ dgu, int T, int F) {
   const int64_t n = (int64_t)T * F;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
     const int64_t t = i / F, d = i - t * F;
-    const float g = ldv(gu + t * 2 * F + d), u = ldv(gu + t * 2 * F + F + d), da = dA[i];
+    const float g = ldv(gu + t * 2 * F + d), u = ldv(gu + t * 2 * F + F + d), da = ldv(dA + i);
     const float sig = 1.f / (1.f + expf(-g));
     st(dgu + t * 2 * F + F + d, da * (g * sig));
     st(dgu + t * 2 * F + d, da * (sig * (1.f + g * (1.f - sig))) * u);
@@ -434,10 +458,10 @@ int swiglu_fused_forward(const void* gu, void* act, int T, int F, int bf16, hipS
   SMHIP_CHECK_LAUNCH();
   return SMHIP_OK;
 }
-int swiglu_fused_backward(const float* dA, const void* gu, void* dgu, int T, int F, int bf16, hipStream_t s) {
+int swiglu_fused_backward(const void* dA, const void* gu, void* dgu, int T, int F, int bf16, hipStream_t s) {
   const int g = gridn((int64_t)T * F);
-  if (bf16) hipLaunchKernelGGL((swiglu_fused_bwd_kernel<uint16_t, uint16_t>), dim3(g), dim3(256), 0, s, dA, (const uint16_t*)gu, (uint16_t*)dgu, T, F);
-  else hipLaunchKernelGGL((swiglu_fused_bwd_kernel<float, float>), dim3(g), dim3(256), 0, s, dA, (const float*)gu, (float*)dgu, T, F);
+  if (bf16) hipLaunchKernelGGL((swiglu_fused_bwd_kernel<uint16_t, uint16_t, uint16_t>), dim3(g), dim3(256), 0, s, (const uint16_t*)dA, (const uint16_t*)gu, (uint16_t*)dgu, T, F);
+  else hipLaunchKernelGGL((swiglu_fused_bwd_kernel<float, float, float>), dim3(g), dim3(256), 0, s, (const float*)dA, (const float*)gu, (float*)dgu, T, F);
   SMHIP_CHECK_LAUNCH();
   return SMHIP_OK;
 }

@@ -104,15 +104,16 @@ int attention_probs_backward(const float* dO, const float* q, const float* k, co
                              const float* probs, float* dq, float* dk, float* dv, int B, int S, int Hq,
                              int Hkv, int D, hipStream_t s);
 // engine_kernels.hip
-int qkv_prep_forward(const float* qkv, void* q, void* k, void* v, float* rinv, const float* wq,
+int qkv_prep_forward(const void* qkv, int qkv_bf16, void* q, void* k, void* v, float* rinv, const float* wq,
                      const float* wk, const float* cosT, const float* sinT, int T, int S, int Hq, int Hkv,
                      int D, int qk_norm, int neox, float eps, int bf16, hipStream_t s);
-int qkv_prep_backward(const float* dq, const float* dk, const float* dv, const float* qkv, const float* rinv,
+int qkv_prep_backward(const float* dq, const float* dk, const float* dv, const void* qkv, int qkv_bf16,
+                      const float* rinv,
                       const float* wq, const float* wk, float* dwq, float* dwk, const float* cosT,
                       const float* sinT, void* dqkv, int T, int S, int Hq, int Hkv, int D, int qk_norm,
                       int neox, int bf16, hipStream_t s);
 int swiglu_fused_forward(const void* gu, void* act, int T, int F, int bf16, hipStream_t s);
-int swiglu_fused_backward(const float* dA, const void* gu, void* dgu, int T, int F, int bf16, hipStream_t s);
+int swiglu_fused_backward(const void* dA, const void* gu, void* dgu, int T, int F, int bf16, hipStream_t s);
 int lora_mask(float* dB, int nr, int r, int Out, const int* col_starts_dev, int nblocks, hipStream_t s);
 int clip_grads(float* g, int64_t n, const float* norm_sq, float max_norm, hipStream_t s);
 int cast_bf16(const float* x, uint16_t* y, int64_t n, hipStream_t s);
