@@ -238,8 +238,15 @@ def main():
         k_ms, k_n, k_fl = all_ms, all_n, all_fl
         kname = "gemm_kernel (all linears, fwd+bwd)"
     achieved = tf(k_fl, k_ms) or 0.0
+    sustained = None
+    if cfg.precision == PREC_BF16:  # what the matrix cores sustain on this device (register operands)
+        v = ctypes.c_double()
+        check(L.smhip_probe_mfma_bf16(ctypes.byref(v)))
+        sustained = round(v.value, 1)
     roofline = {"bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
                 "frac": round(achieved / peak, 4), "traffic": gemm_dx_traffic() if dx_n else None,
+                "mfma_sustained_tflops": sustained,
+                "frac_of_sustained": round(achieved / sustained, 4) if sustained else None,
                 "kernel": kname,
                 "launches_per_step": k_n / psteps, "avg_launch_us": round(k_ms / k_n * 1e3, 2) if k_n else None,
                 "algorithmic_flops_per_launch": round(k_fl / k_n) if k_n else None,

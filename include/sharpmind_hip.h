@@ -257,6 +257,10 @@ int smhip_engine_read_activation(void* engine, const char* what, int layer, void
  * quantised column-plane B operand, i.e. the backward dX products through the frozen base), c < ncat. */
 int smhip_profile_begin(int max_events);
 int smhip_profile_end(double* out, int ncat);
+/* Measurement, no reference counterpart: the bf16 MFMA rate (TFLOP/s) the device sustains with register
+ * operands and no memory traffic, one 8-wave workgroup per CU (about 0.1 s).  bench.py reports it
+ * beside the published dense peak. */
+int smhip_probe_mfma_bf16(double* tflops);
 /* Uniform random token ids in [0, vocab) (synthetic batches). */
 int smhip_fill_token_ids(int32_t* ids, int64_t n, uint64_t seed, int vocab, smhip_stream_t stream);
 
