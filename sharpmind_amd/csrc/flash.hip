@@ -56,33 +56,6 @@ __device__ inline bf16x8 tload(const uint16_t* row, int c16, int lane) {
   return as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
 }
 
-// Stage rows [r0, r0+NR) x D of a bf16 matrix into LDS as [NR][D+8] and/or transposed [D][NR+8].
-template <int D, int NR, bool ROWS, bool TRANS, int NT = 256>
-__device__ inline void stage(const uint16_t* __restrict__ g, int64_t ld, int r0, uint16_t* sRow,
-                             uint16_t* sT) {
-  constexpr int RP = D + 8, TP = NR + 4;
-  if constexpr (ROWS) {
-    for (int c = threadIdx.x; c < NR * D / 8; c += NT) {
-      const int r = c / (D / 8), dc = (c % (D / 8)) * 8;
-      *reinterpret_cast<uint4*>(sRow + r * RP + dc) = *reinterpret_cast<const uint4*>(g + (int64_t)(r0 + r) * ld + dc);
-    }
-  }
-  if constexpr (TRANS) {
-    for (int c = threadIdx.x; c < (NR / 2) * (D / 8); c += NT) {
-      const int rp = c % (NR / 2), dc = (c / (NR / 2)) * 8;
-      uint4 a = *reinterpret_cast<const uint4*>(g + (int64_t)(r0 + 2 * rp) * ld + dc);
-      uint4 b = *reinterpret_cast<const uint4*>(g + (int64_t)(r0 + 2 * rp + 1) * ld + dc);
-      const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        uint32_t lo = (j & 1) ? (av[j >> 1] >> 16) : (av[j >> 1] & 0xFFFFu);
-        uint32_t hi = (j & 1) ? (bv[j >> 1] >> 16) : (bv[j >> 1] & 0xFFFFu);
-        *reinterpret_cast<uint32_t*>(sT + (dc + j) * TP + 2 * rp) = lo | (hi << 16);
-      }
-    }
-  }
-}
-
 // Register-prefetched staging: load() issues the global reads of a [NR][D] row tile (pairs
 // of rows per 16-byte column chunk) into registers, store() writes them to LDS as [NR][D+8]
 // and/or transposed [D][NR+8].  Loading tile t+1 before the MFMAs of tile t hides the
@@ -134,7 +107,8 @@ struct Pref {
 };
 
 // ============================================================================
-// forward: grid (S/128, Hq, B), 4 waves x 32 queries, key tiles of 64.
+// forward: grid (S/128, Hq, B), 4 waves x 32 queries, key tiles of 64 (the next one loaded into
+// registers while the current one is multiplied).
 // PAIR (S/128 even): grid (S/256, Hq, B) of 8 waves; waves 0-3 take query block nb-1-x and
 // waves 4-7 block x, so every workgroup (and every SIMD, which hosts wave s and wave s+4)
 // carries the same causal work and the two blocks share the staged K/V tiles.  Without it
@@ -171,11 +145,18 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_fwd_kernel(const uint16_t
   const int kend = (nb - (int)blockIdx.x) * 128;  // the longer block of the workgroup
   const int wq_last = qb * 128 + w * 32 + 31;  // last query of this wave
 
+  Pref<D, KB, NT> pk, pv;
+  pk.load(kb, ldk, 0);
+  pv.load(vb, ldv, 0);
   for (int k0 = 0; k0 < kend; k0 += KB) {
     __syncthreads();
-    stage<D, KB, true, false, NT>(kb, ldk, k0, sK, nullptr);
-    stage<D, KB, false, true, NT>(vb, ldv, k0, nullptr, sVt);
+    pk.template store<true, false>(sK, nullptr);
+    pv.template store<false, true>(nullptr, sVt);
     __syncthreads();
+    if (k0 + KB < kend) {  // next tile in flight during this tile's MFMAs
+      pk.load(kb, ldk, k0 + KB);
+      pv.load(vb, ldv, k0 + KB);
+    }
     if (k0 > wq_last) continue;  // whole tile masked for this wave
     floatx16 sacc[2];
     zero16(sacc[0]);

@@ -450,6 +450,16 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW, ST>::OCC)) void ge
     }
   };
 
+  // one tile of the rank extension [A2 | B2] (K2 columns), staged with ordinary loads into
+  // stage buf, which no main tile uses until the barrier that ends the step
+  auto ext_step = [&](int buf, int t) {
+    ext_tile<BM, NT>(g.amode2, g.ext_vec != 0, g.A2, m0, t * BK, g.M, g.K2, g.alpha2, sA(buf));
+    ext_tile<BN, NT>(g.bmode2, g.ext_vec != 0, g.B2, n0, t * BK, g.N, g.K2, 1.f, sB(buf));
+    __syncthreads();
+    compute(buf, [] {});
+    __syncthreads();
+  };
+
   if constexpr (ST > 2) {
     // ST-stage ring (direct-to-LDS operands only): tiles t+1 .. t+ST-2 are in flight while
     // tile t is multiplied; the barrier at the top of iteration t also frees the stage of
@@ -462,6 +472,8 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW, ST>::OCC)) void ge
         la.fetch(sA(t), (kt0 + t) * BK);
         lb.fetch(sB(t), (kt0 + t) * BK);
       }
+    // the rank extension runs first, from the stage the ring fills last, while the first tiles land
+    for (int t = 0; t < nk2; t++) ext_step(ST - 1, t);
     for (int t = 0; t < nk1; t++) {
       if (t + ST - 2 < nk1) wait_vm_n<(ST - 2) * PER>();
       else wait_vm();
@@ -474,10 +486,10 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW, ST>::OCC)) void ge
         }
       });
     }
-    if (nk2 > 0) __syncthreads();
   } else if (nk1 > 0) {
     la.fetch(sA(0), kt0 * BK);
     lb.fetch(sB(0), kt0 * BK);
+    for (int t = 0; t < nk2; t++) ext_step(1, t);  // overlaps the first tile's loads
     la.commit(sA(0));
     lb.commit(sB(0));
     wait_vm();
@@ -499,13 +511,8 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW, ST>::OCC)) void ge
       __syncthreads();
     }
   }
-  for (int t = 0; t < nk2; t++) {  // rank extension (all waves are past the last main-tile barrier)
-    ext_tile<BM, NT>(g.amode2, g.ext_vec != 0, g.A2, m0, t * BK, g.M, g.K2, g.alpha2, sA(0));
-    ext_tile<BN, NT>(g.bmode2, g.ext_vec != 0, g.B2, n0, t * BK, g.N, g.K2, 1.f, sB(0));
-    __syncthreads();
-    compute(0, [] {});
-    __syncthreads();
-  }
+  if (nk1 == 0)
+    for (int t = 0; t < nk2; t++) ext_step(0, t);
 
   // epilogue: lane holds column (lane&31) and rows (e/4)*8 + (lane>>5)*4 + e%4 of each 32x32 block.
   // Whole tiles take a branch-free path, one instantiation per combination of the uniform
