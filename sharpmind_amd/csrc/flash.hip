@@ -262,6 +262,9 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_bwd_dkdv_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t sdOt[D * TP];
   __shared__ __attribute__((aligned(16))) float sL[QB];
   __shared__ __attribute__((aligned(16))) float sDi[QB];
+  // each wave's 32 V rows: read as the B operand of dP = dO V^T from LDS rather than held in
+  // registers, which keeps the wave within 256 registers (no spills in the query loop)
+  __shared__ __attribute__((aligned(16))) uint16_t sV[(NT / 64) * 32 * RP];
   // key block of 128; PAIR: waves 0-3 take key block x (the most queries), waves 4-7 block nb-1-x
   const int nb = PAIR ? 2 * (int)gridDim.x : (int)gridDim.x;
   const int half = PAIR ? (int)(threadIdx.x >> 8) : 0;
@@ -271,14 +274,16 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_bwd_dkdv_kernel(
   const int kw0 = kbk * 128 + w * 32;
   const int kj = kw0 + (lane & 31);  // this lane's key (B-operand column)
 
-  bf16x8 kf[D / 16], vf[D / 16];
+  bf16x8 kf[D / 16];
+  uint16_t* sVw = sV + (threadIdx.x >> 6) * 32 * RP;  // this wave's rows: key kw0 + row
   {
     const uint16_t* krow = k + ((int64_t)b * S + kj) * ldk + kvh * D + (lane >> 5) * 8;
     const uint16_t* vrow = v + ((int64_t)b * S + kj) * ldv + kvh * D + (lane >> 5) * 8;
 #pragma unroll
     for (int kk = 0; kk < D / 16; kk++) {
       kf[kk] = as_bf16x8(*reinterpret_cast<const uint4*>(krow + kk * 16));
-      vf[kk] = as_bf16x8(*reinterpret_cast<const uint4*>(vrow + kk * 16));
+      *reinterpret_cast<uint4*>(sVw + (lane & 31) * RP + kk * 16 + (lane >> 5) * 8) =
+          *reinterpret_cast<const uint4*>(vrow + kk * 16);
     }
   }
   floatx16 dv[D / 32], dk[D / 32];
@@ -318,7 +323,8 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_bwd_dkdv_kernel(
       for (int kk = 0; kk < D / 16; kk++) {
         const int off = (jb * 32 + (lane & 31)) * RP + kk * 16 + (lane >> 5) * 8;
         sacc = mfma16(as_bf16x8(*reinterpret_cast<const uint4*>(sQ + off)), kf[kk], sacc);
-        dpacc = mfma16(as_bf16x8(*reinterpret_cast<const uint4*>(sdO + off)), vf[kk], dpacc);
+        const bf16x8 vf = as_bf16x8(*reinterpret_cast<const uint4*>(sVw + (lane & 31) * RP + kk * 16 + (lane >> 5) * 8));
+        dpacc = mfma16(as_bf16x8(*reinterpret_cast<const uint4*>(sdO + off)), vf, dpacc);
       }
       // this lane's 16 rows are 4 runs of 4 consecutive queries: row statistics as float4
       const bool diag = q0 + jb * 32 < kw0 + 31;  // some query of the block precedes some key
@@ -347,6 +353,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_bwd_dkdv_kernel(
           dv[i] = mfma16(pf, tload(sdOt + (i * 32 + (lane & 31)) * TP, jb * 32 + c * 16, lane), dv[i]);
           dk[i] = mfma16(sf, tload(sQt + (i * 32 + (lane & 31)) * TP, jb * 32 + c * 16, lane), dk[i]);
         }
+        __builtin_amdgcn_sched_barrier(0);  // bounds the transposed fragments in flight
       }
     }
   }
