@@ -280,9 +280,27 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
     const float* __restrict__ dq, const float* __restrict__ dk, const float* __restrict__ dv,
     const TQ* __restrict__ qkv, const float* __restrict__ rinv, const float* __restrict__ wq,
     const float* __restrict__ wk, const float* __restrict__ cosT, const float* __restrict__ sinT,
-    TA* __restrict__ dqkv, float* __restrict__ part, int T, int S, int Hq, int Hkv, int qk_norm, int neox) {
+    TA* __restrict__ dqkv, float* __restrict__ part, int T, int S, int Hq, int Hkv, int qk_norm, int neox,
+    int kv_grp) {
   constexpr int E = D / 32, P = D / 2;
   const int l = threadIdx.x & 31, hw = threadIdx.x >> 5;  // half-wave 0..7
+  // kv_grp > 0: dk / dv are the attention backward's per-query-head partials [T, Hq, D]; a KV
+  // head's gradient is the sum of its kv_grp query heads, added in ascending head order
+  auto ld_kv = [&](const float* base, int t, int kvh, float* g) {
+    if (kv_grp == 0) {
+      ldE<E>(base + (int64_t)t * Hkv * D + kvh * D + l * E, g);
+      return;
+    }
+    const float* p0 = base + ((int64_t)t * Hq + (int64_t)kvh * kv_grp) * D + l * E;
+    float h[E];
+#pragma unroll
+    for (int i = 0; i < E; i++) g[i] = 0.f;
+    for (int j = 0; j < kv_grp; j++) {
+      ldE<E>(p0 + (int64_t)j * D, h);
+#pragma unroll
+      for (int i = 0; i < E; i++) g[i] += h[i];
+    }
+  };
   const int H = Hq + 2 * Hkv, nqkv = H * D;
   const int64_t rows = (int64_t)T * H;
   float aq[E], ak[E];
@@ -295,12 +313,13 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
     TA* dst = dqkv + (int64_t)t * nqkv + hh * D + l * E;
     float g[E];
     if (hh >= Hq + Hkv) {
-      ldE<E>(dv + (int64_t)t * Hkv * D + (hh - Hq - Hkv) * D + l * E, g);
+      ld_kv(dv, t, hh - Hq - Hkv, g);
       if (live) stE<E>(dst, g);
       continue;
     }
     const bool isq = hh < Hq;
-    ldE<E>((isq ? dq + (int64_t)t * Hq * D + hh * D : dk + (int64_t)t * Hkv * D + (hh - Hq) * D) + l * E, g);
+    if (isq) ldE<E>(dq + (int64_t)t * Hq * D + hh * D + l * E, g);
+    else ld_kv(dk, t, hh - Hq, g);
     const int pos = t % S;
     float gr[E];
     if (neox) {
@@ -393,8 +412,10 @@ int qkv_prep_backward(const float* dq, const float* dk, const float* dv, const v
                       const float* rinv,
                       const float* wq, const float* wk, float* dwq, float* dwk, const float* cosT,
                       const float* sinT, void* dqkv, int T, int S, int Hq, int Hkv, int D, int qk_norm,
-                      int neox, int bf16, hipStream_t s) {
+                      int neox, int bf16, int kv_grp, hipStream_t s) {
   SMHIP_REQUIRE(D <= 128 && D % 2 == 0, "qkv prep: head_dim must be even and <= 128");
+  SMHIP_REQUIRE(kv_grp == 0 || ((D == 128 || D == 64) && kv_grp * Hkv == Hq),
+                "qkv prep: per-query-head K/V partials need head_dim 64 or 128 and kv_grp = Hq / Hkv");
   const int64_t rows = (int64_t)T * (Hq + 2 * Hkv);
   const bool want_dw = qk_norm && (dwq || dwk);
   const bool vec = D == 128 || D == 64;
@@ -409,7 +430,7 @@ int qkv_prep_backward(const float* dq, const float* dk, const float* dv, const v
   SMHIP_REQUIRE(bf16 || !qkv_bf16, "qkv prep: bf16 projections need bf16 outputs");
   if (vec) {
 #define SMHIP_QKV_BWD(DD, TT, TQ) \
-  hipLaunchKernelGGL((qkv_prep_bwd_vec_kernel<DD, TT, TQ>), dim3(g), dim3(256), 0, s, dq, dk, dv, (const TQ*)qkv, rinv, wq, wk, cosT, sinT, (TT*)dqkv, part, T, S, Hq, Hkv, qk_norm, neox)
+  hipLaunchKernelGGL((qkv_prep_bwd_vec_kernel<DD, TT, TQ>), dim3(g), dim3(256), 0, s, dq, dk, dv, (const TQ*)qkv, rinv, wq, wk, cosT, sinT, (TT*)dqkv, part, T, S, Hq, Hkv, qk_norm, neox, kv_grp)
     if (qkv_bf16) { if (D == 128) SMHIP_QKV_BWD(128, uint16_t, uint16_t); else SMHIP_QKV_BWD(64, uint16_t, uint16_t); }
     else if (D == 128) { if (bf16) SMHIP_QKV_BWD(128, uint16_t, float); else SMHIP_QKV_BWD(128, float, float); }
     else { if (bf16) SMHIP_QKV_BWD(64, uint16_t, float); else SMHIP_QKV_BWD(64, float, float); }

@@ -509,12 +509,19 @@ size_t flash_backward_workspace(int B, int S, int Hq, int D) {
   return sizeof(float) * ((size_t)B * Hq * S + 2 * (size_t)B * S * Hq * D) + 256;
 }
 
+void flash_backward_partials(void* ws, int B, int S, int Hq, int D, const float** dKh, const float** dVh) {
+  const float* Di = (const float*)ws;
+  *dKh = Di + (size_t)B * Hq * S;
+  *dVh = *dKh + (size_t)B * S * Hq * D;
+}
+
 int flash_backward(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
                    const uint16_t* dO, const float* lse, float* dq, float* dk, float* dv, int B, int S,
                    int Hq, int Hkv, int D, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, int64_t lddo,
                    int64_t lddq, int64_t lddk, int64_t lddv, void* ws, hipStream_t s) {
   SMHIP_REQUIRE(S % 128 == 0, "flash attention: S must be a multiple of 128");
   SMHIP_REQUIRE(Hkv > 0 && Hq % Hkv == 0, "flash attention: Hq must be a multiple of Hkv");
+  SMHIP_REQUIRE((dk == nullptr) == (dv == nullptr), "flash attention backward: dk and dv are both given or both null");
   const float scale = 1.f / sqrtf((float)D), sl2 = kLog2e * scale;
   float* Di = (float*)ws;
   float* dKh = Di + (size_t)B * Hq * S;
@@ -531,8 +538,9 @@ int flash_backward(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
                      Hkv, ldq, ldk, ldv, lddo, sl2, scale);                                                     \
   hipLaunchKernelGGL((fa_bwd_dq_kernel<DD, PP>), grid, block, 0, s, q, k, v, dO, lse, Di, dq, S, Hq, Hkv, ldq, \
                      ldk, ldv, lddo, lddq, sl2, scale);                                                         \
-  hipLaunchKernelGGL(fa_group_reduce_kernel<DD>, dim3(gred), dim3(256), 0, s, dKh, dVh, dk, dv, B, S, Hq, Hkv,  \
-                     lddk, lddv);
+  if (dk)                                                                                                       \
+    hipLaunchKernelGGL(fa_group_reduce_kernel<DD>, dim3(gred), dim3(256), 0, s, dKh, dVh, dk, dv, B, S, Hq, Hkv, \
+                       lddk, lddv);
   if (D == 128) { if (pair) { FA_BWD(128, true) } else { FA_BWD(128, false) } }
   else if (D == 64) { if (pair) { FA_BWD(64, true) } else { FA_BWD(64, false) } }
   else return fail(SMHIP_EUNSUPPORTED, "flash attention: head_dim must be 64 or 128");

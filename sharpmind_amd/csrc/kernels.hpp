@@ -95,6 +95,9 @@ int flash_forward(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint1
                   int S, int Hq, int Hkv, int D, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
                   hipStream_t s);
 size_t flash_backward_workspace(int B, int S, int Hq, int D);
+// dk == dv == nullptr: flash_backward leaves the per-query-head partials dK_h, dV_h [B*S, Hq, D]
+// (fp32) in the workspace instead of summing each GQA group; these are their addresses
+void flash_backward_partials(void* ws, int B, int S, int Hq, int D, const float** dKh, const float** dVh);
 int flash_backward(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
                    const uint16_t* dO, const float* lse, float* dq, float* dk, float* dv, int B, int S,
                    int Hq, int Hkv, int D, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, int64_t lddo,
@@ -111,7 +114,7 @@ int qkv_prep_backward(const float* dq, const float* dk, const float* dv, const v
                       const float* rinv,
                       const float* wq, const float* wk, float* dwq, float* dwk, const float* cosT,
                       const float* sinT, void* dqkv, int T, int S, int Hq, int Hkv, int D, int qk_norm,
-                      int neox, int bf16, hipStream_t s);
+                      int neox, int bf16, int kv_grp, hipStream_t s);
 int swiglu_fused_forward(const void* gu, void* act, int T, int F, int bf16, hipStream_t s);
 int swiglu_fused_backward(const void* dA, const void* gu, void* dgu, int T, int F, int bf16, hipStream_t s);
 int lora_mask(float* dB, int nr, int r, int Out, const int* col_starts_dev, int nblocks, hipStream_t s);
