@@ -79,3 +79,28 @@ def test_qgemm_bf16(orc, dev, qtype, trans, M, N, K):
     torch.cuda.synchronize()
     ref = a.astype(np.float64) @ (wb if trans else wb.T)
     assert rel_err(tc.cpu().numpy(), ref) <= 1e-5, rel_err(tc.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("M,N,K,am,bm", [(6144, 32, 4096, 3, 3), (4096, 48, 4096, 2, 2), (1024, 16, 4096, 3, 3),
+                                         (48, 4096, 4096, 2, 2)])
+def test_skinny_split_reduction_repeatable(dev, M, N, K, am, bm):
+    """Rank-sized products split K across workgroups and add the splits in a fixed order:
+    back-to-back calls on one stream give the same bits, and each matches float64."""
+    rng = np.random.default_rng(M + N)
+    a = _rnd((M, K), rng)
+    b = _rnd((N, K), rng)
+    c0 = _rnd((M, N), rng)
+    ta = torch.from_numpy(np.ascontiguousarray(a if am % 2 == 0 else a.T)).to(dev).to(torch.bfloat16)
+    tb = torch.from_numpy(np.ascontiguousarray(b if bm % 2 == 0 else b.T)).to(dev).to(torch.bfloat16)
+    lda = K if am % 2 == 0 else M
+    ldb = K if bm % 2 == 0 else N
+    ref = 0.25 * (a.astype(np.float64) @ b.astype(np.float64).T) + c0
+    outs = []
+    for _ in range(3):
+        tc = torch.from_numpy(c0).to(dev)
+        check(sharpmind_amd.lib().smhip_gemm(M, N, K, am, ta.data_ptr(), lda, bm, tb.data_ptr(), ldb, 0.25, 1.0,
+                                             tc.data_ptr(), N, 0, 0, 1, torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        outs.append(tc.cpu().numpy())
+        assert rel_err(outs[-1], ref) <= 1e-5
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[1], outs[2])
