@@ -373,6 +373,100 @@ struct Shape {
   static constexpr int OCC = LDS * 2 <= 160 * 1024 && MB * NB <= 8 && NW == 4 ? 2 : 1;
 };
 
+// Epilogue of a BM x BN tile (layout S): lane holds column (lane&31) and rows
+// (e/4)*8 + (lane>>5)*4 + e%4 of each 32x32 accumulator block.
+template <class S, bool C_BF16>
+__device__ __forceinline__ void gemm_epilogue(const Args& g, floatx16 (&acc)[S::MB][S::NB], int m0, int n0, int split) {
+  constexpr int MB = S::MB, NB = S::NB, BM = S::WM * (S::NT / 64 / S::WGN), BN = S::WN * S::WGN;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int wm = wv / S::WGN, wn = wv % S::WGN;
+  // Whole tiles take a branch-free path, one instantiation per combination of the uniform
+  // options: the general path below tests every element and is several times the code, which a
+  // workgroup runs once, from a cold instruction cache
+  if (m0 + BM <= g.M && n0 + BN <= g.N) {
+    const int r0 = m0 + wm * S::WM + (lane >> 5) * 4, c0 = n0 + wn * S::WN + (lane & 31);
+    auto store = [&](auto has_bias, auto has_r, auto has_beta) {
+#pragma unroll
+      for (int j = 0; j < NB; j++) {
+        const int col = c0 + j * 32;
+        float bv = 0.f;
+        if constexpr (decltype(has_bias)::value) bv = g.bias[col];
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+          for (int e = 0; e < 16; e++) {
+            const int64_t row = r0 + i * 32 + (e >> 2) * 8 + (e & 3);
+            float o = g.alpha * acc[i][j][e];
+            if constexpr (decltype(has_bias)::value) o = o + bv;
+            if constexpr (C_BF16) {
+              uint16_t* c = (uint16_t*)g.C + row * g.ldc + col;
+              if constexpr (decltype(has_beta)::value) o = o + g.beta * bf2f(*c);
+              *c = f2bf(o);
+            } else {
+              float* c = (float*)g.C + row * g.ldc + col;
+              if constexpr (decltype(has_r)::value) o = o + g.R[row * g.ldr + col];
+              if constexpr (decltype(has_beta)::value) o = o + g.beta * *c;
+              *c = o;
+            }
+            // one 32x32 block at a time: hoisting every block's R / C loads spills the accumulators
+            if (e == 15) __builtin_amdgcn_sched_barrier(0);
+          }
+      }
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    if (g.partial) {
+      float* p = g.partial + (int64_t)split * g.M * g.N;
+#pragma unroll
+      for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+#pragma unroll
+          for (int e = 0; e < 16; e++)
+            p[(int64_t)(r0 + i * 32 + (e >> 2) * 8 + (e & 3)) * g.N + c0 + j * 32] = acc[i][j][e];
+      return;
+    }
+    const bool bias = g.bias != nullptr, r = !C_BF16 && g.R != nullptr, beta = g.beta != 0.f;
+    if (!bias && !r && !beta) store(F{}, F{}, F{});
+    else if (!bias && r && !beta) store(F{}, T{}, F{});
+    else if (!bias && !r && beta) store(F{}, F{}, T{});
+    else if (bias && !r && !beta) store(T{}, F{}, F{});
+    else if (bias && r && !beta) store(T{}, T{}, F{});
+    else if (!bias && r && beta) store(F{}, T{}, T{});
+    else if (bias && !r && beta) store(T{}, F{}, T{});
+    else store(T{}, T{}, T{});
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < MB; i++)
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const int col = n0 + wn * S::WN + j * 32 + (lane & 31);
+      if (col >= g.N) continue;
+      const float bv = g.bias ? g.bias[col] : 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int row = m0 + wm * S::WM + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        if (row >= g.M) continue;
+        if (g.partial) {
+          g.partial[((int64_t)split * g.M + row) * g.N + col] = acc[i][j][e];
+          continue;
+        }
+        float o = g.alpha * acc[i][j][e] + bv;
+        if constexpr (C_BF16) {
+          uint16_t* c = (uint16_t*)g.C + (int64_t)row * g.ldc + col;
+          if (g.beta != 0.f) o = o + g.beta * bf2f(*c);
+          *c = f2bf(o);
+        } else {
+          float* c = (float*)g.C + (int64_t)row * g.ldc + col;
+          if (g.R) o = o + g.R[(int64_t)row * g.ldr + col];
+          if (g.beta != 0.f) o = o + g.beta * *c;
+          *c = o;
+        }
+      }
+    }
+}
+
 // TAG only names the instantiation (1: the backward dX products through the frozen base, so
 // profilers can tell them from the forward GEMMs that share the code)
 template <int BM, int BN, int WGM, int NW, int AMODE, int BMODE, bool C_BF16, int ST = 2, int TAG = 0>
@@ -514,92 +608,7 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW, ST>::OCC)) void ge
   if (nk1 == 0)
     for (int t = 0; t < nk2; t++) ext_step(0, t);
 
-  // epilogue: lane holds column (lane&31) and rows (e/4)*8 + (lane>>5)*4 + e%4 of each 32x32 block.
-  // Whole tiles take a branch-free path, one instantiation per combination of the uniform
-  // options: the general path below tests every element and is several times the code, which a
-  // workgroup runs once, from a cold instruction cache
-  if (m0 + BM <= g.M && n0 + BN <= g.N) {
-    const int r0 = m0 + wm * S::WM + (lane >> 5) * 4, c0 = n0 + wn * S::WN + (lane & 31);
-    auto store = [&](auto has_bias, auto has_r, auto has_beta) {
-#pragma unroll
-      for (int j = 0; j < NB; j++) {
-        const int col = c0 + j * 32;
-        float bv = 0.f;
-        if constexpr (decltype(has_bias)::value) bv = g.bias[col];
-#pragma unroll
-        for (int i = 0; i < MB; i++)
-#pragma unroll
-          for (int e = 0; e < 16; e++) {
-            const int64_t row = r0 + i * 32 + (e >> 2) * 8 + (e & 3);
-            float o = g.alpha * acc[i][j][e];
-            if constexpr (decltype(has_bias)::value) o = o + bv;
-            if constexpr (C_BF16) {
-              uint16_t* c = (uint16_t*)g.C + row * g.ldc + col;
-              if constexpr (decltype(has_beta)::value) o = o + g.beta * bf2f(*c);
-              *c = f2bf(o);
-            } else {
-              float* c = (float*)g.C + row * g.ldc + col;
-              if constexpr (decltype(has_r)::value) o = o + g.R[row * g.ldr + col];
-              if constexpr (decltype(has_beta)::value) o = o + g.beta * *c;
-              *c = o;
-            }
-            // one 32x32 block at a time: hoisting every block's R / C loads spills the accumulators
-            if (e == 15) __builtin_amdgcn_sched_barrier(0);
-          }
-      }
-    };
-    using T = std::true_type;
-    using F = std::false_type;
-    if (g.partial) {
-      float* p = g.partial + (int64_t)split * g.M * g.N;
-#pragma unroll
-      for (int i = 0; i < MB; i++)
-#pragma unroll
-        for (int j = 0; j < NB; j++)
-#pragma unroll
-          for (int e = 0; e < 16; e++)
-            p[(int64_t)(r0 + i * 32 + (e >> 2) * 8 + (e & 3)) * g.N + c0 + j * 32] = acc[i][j][e];
-      return;
-    }
-    const bool bias = g.bias != nullptr, r = !C_BF16 && g.R != nullptr, beta = g.beta != 0.f;
-    if (!bias && !r && !beta) store(F{}, F{}, F{});
-    else if (!bias && r && !beta) store(F{}, T{}, F{});
-    else if (!bias && !r && beta) store(F{}, F{}, T{});
-    else if (bias && !r && !beta) store(T{}, F{}, F{});
-    else if (bias && r && !beta) store(T{}, T{}, F{});
-    else if (!bias && r && beta) store(F{}, T{}, T{});
-    else if (bias && !r && beta) store(T{}, F{}, T{});
-    else store(T{}, T{}, T{});
-    return;
-  }
-#pragma unroll
-  for (int i = 0; i < MB; i++)
-#pragma unroll
-    for (int j = 0; j < NB; j++) {
-      const int col = n0 + wn * S::WN + j * 32 + (lane & 31);
-      if (col >= g.N) continue;
-      const float bv = g.bias ? g.bias[col] : 0.f;
-#pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const int row = m0 + wm * S::WM + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-        if (row >= g.M) continue;
-        if (g.partial) {
-          g.partial[((int64_t)split * g.M + row) * g.N + col] = acc[i][j][e];
-          continue;
-        }
-        float o = g.alpha * acc[i][j][e] + bv;
-        if constexpr (C_BF16) {
-          uint16_t* c = (uint16_t*)g.C + (int64_t)row * g.ldc + col;
-          if (g.beta != 0.f) o = o + g.beta * bf2f(*c);
-          *c = f2bf(o);
-        } else {
-          float* c = (float*)g.C + (int64_t)row * g.ldc + col;
-          if (g.R) o = o + g.R[(int64_t)row * g.ldr + col];
-          if (g.beta != 0.f) o = o + g.beta * *c;
-          *c = o;
-        }
-      }
-    }
+  gemm_epilogue<S, C_BF16>(g, acc, m0, n0, split);
 }
 
 // float4 form (N % 4 == 0, ldc / ldr % 4 == 0): 4 consecutive columns per thread, the
