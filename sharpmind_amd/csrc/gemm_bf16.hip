@@ -686,10 +686,11 @@ __global__ void splitk_epilogue_kernel(const float* __restrict__ partial, int sp
 }
 
 // ---------------------------------------------------------------- host dispatch
-// 256x256 runs 8 waves (2 x 4, each 128 x 64); the others 4 waves.  64x128 and 128x64 are
+// 256x256 runs 8 waves (2 x 4, each 128 x 64), 256x192 8 waves (4 x 2, each 64 x 96, for
+// N = 3072: one tile per CU at M = 4096), 128x128W8 8 waves; the others 4.  64x128 and 128x64 are
 // for skinny products (LoRA rank on one side), which are bandwidth-bound: many small
 // workgroups plus split-K keep every CU streaming.
-enum TileId { T256x256 = 0, T256x128 = 1, T128x128 = 2, T256x64 = 3, T64x128 = 4, T128x64 = 5, T128x128W8 = 6, NTILE = 7 };
+enum TileId { T256x256 = 0, T256x128 = 1, T128x128 = 2, T256x64 = 3, T64x128 = 4, T128x64 = 5, T128x128W8 = 6, T256x192 = 7, NTILE = 8 };
 struct TileInfo { int bm, bn, occ; double eff; };
 // eff: relative MFMA throughput per CU of the tile shape (larger tiles re-read less LDS/L2)
 static const TileInfo kTiles[NTILE] = {
@@ -700,6 +701,7 @@ static const TileInfo kTiles[NTILE] = {
     {64, 128, Shape<64, 128, 1, 4>::OCC, 0.50},
     {128, 64, Shape<128, 64, 4, 4>::OCC, 0.50},
     {128, 128, Shape<128, 128, 2, 8>::OCC, 0.88},
+    {256, 192, Shape<256, 192, 4, 8>::OCC, 0.87},  // one tile per CU at 4096 x 3072: 840 TF/s vs 743
 };
 
 // ring depth of the direct-to-LDS 128x128 kernels: 3 stages for the 8-wave tile (one
@@ -738,6 +740,7 @@ static void launch_tile(int tile, const Args& a, int c_bf16, int sp, hipStream_t
     case T256x64: launch_c<256, 64, 4, 4, AM, BMD, TAG>(a, c_bf16, sp, s); break;
     case T64x128: launch_c<64, 128, 1, 4, AM, BMD, TAG>(a, c_bf16, sp, s); break;
     case T128x128W8: launch_c<128, 128, 2, 8, AM, BMD, TAG>(a, c_bf16, sp, s); break;
+    case T256x192: launch_c<256, 192, 4, 8, AM, BMD, TAG>(a, c_bf16, sp, s); break;
     default: launch_c<128, 64, 4, 4, AM, BMD, TAG>(a, c_bf16, sp, s); break;
   }
 }
@@ -778,7 +781,7 @@ static int pick_tile(int M, int N, int splits, int bmode) {
   const int cus = num_cus();
   int best = T128x128;
   double best_t = 1e300;
-  for (int t = 0; t < T64x128; t++) {
+  for (int t : {T256x256, T256x128, T128x128, T256x64, T256x192}) {
     const TileInfo& ti = kTiles[t];
     if (t == T256x64 && N > 64) continue;
     const int64_t tiles = (int64_t)ceil_div(M, ti.bm) * ceil_div(N, ti.bn) * splits;
