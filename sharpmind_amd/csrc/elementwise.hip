@@ -228,11 +228,60 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_fwd_kernel(
   }
 }
 
+// Row in registers (D = 256 * NV, 16-byte aligned rows): one float4 load per lane and chunk,
+// then float4 / 8-byte bf16 stores.  Same per-element arithmetic as rmsnorm_fwd_kernel; the sum
+// of squares runs over each lane's 4*NV elements before the wave reduction.
+template <int NV>
+__global__ __launch_bounds__(kBlock) void rmsnorm_fwd_vec_kernel(
+    const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y,
+    uint16_t* __restrict__ yb, float* __restrict__ rinv, int T, int D, float eps) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  for (int t = blockIdx.x * 4 + wv; t < T; t += gridDim.x * 4) {
+    const float* xr = x + (int64_t)t * D;
+    float4 v[NV];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      v[j] = ld4(xr + (j * 64 + lane) * 4);
+      ss += v[j].x * v[j].x;
+      ss += v[j].y * v[j].y;
+      ss += v[j].z * v[j].z;
+      ss += v[j].w * v[j].w;
+    }
+    ss = wave_sum(ss);
+    const float ri = 1.f / sqrtf(ss / (float)D + eps);
+    if (lane == 0) rinv[t] = ri;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      const int c = (j * 64 + lane) * 4;
+      const float4 g = ld4(w + c);
+      const float4 o = make_float4(v[j].x * ri * g.x, v[j].y * ri * g.y, v[j].z * ri * g.z, v[j].w * ri * g.w);
+      if (y) st4(y + (int64_t)t * D + c, o);
+      if (yb) *reinterpret_cast<uint2*>(yb + (int64_t)t * D + c) = make_uint2(pack_bf2(o.x, o.y), pack_bf2(o.z, o.w));
+    }
+  }
+}
+
 int rmsnorm_forward(const float* x, const float* w, float* y, uint16_t* yb, float* rinv, int T,
                     int D, float eps, hipStream_t s) {
   if (T <= 0) return SMHIP_OK;
-  hipLaunchKernelGGL(rmsnorm_fwd_kernel, dim3(grid_for(T, 4)), dim3(kBlock), 0, s, x, w, y, yb,
-                     rinv, T, D, eps);
+  const bool vec = D % 256 == 0 && D <= 2048 && (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 &&
+                   (!y || (uintptr_t)y % 16 == 0) && (!yb || (uintptr_t)yb % 8 == 0);
+  const dim3 g(grid_for(T, 4)), b(kBlock);
+  if (vec) {
+    switch (D / 256) {
+      case 1: hipLaunchKernelGGL(rmsnorm_fwd_vec_kernel<1>, g, b, 0, s, x, w, y, yb, rinv, T, D, eps); break;
+      case 2: hipLaunchKernelGGL(rmsnorm_fwd_vec_kernel<2>, g, b, 0, s, x, w, y, yb, rinv, T, D, eps); break;
+      case 3: hipLaunchKernelGGL(rmsnorm_fwd_vec_kernel<3>, g, b, 0, s, x, w, y, yb, rinv, T, D, eps); break;
+      case 4: hipLaunchKernelGGL(rmsnorm_fwd_vec_kernel<4>, g, b, 0, s, x, w, y, yb, rinv, T, D, eps); break;
+      case 5: hipLaunchKernelGGL(rmsnorm_fwd_vec_kernel<5>, g, b, 0, s, x, w, y, yb, rinv, T, D, eps); break;
+      case 6: hipLaunchKernelGGL(rmsnorm_fwd_vec_kernel<6>, g, b, 0, s, x, w, y, yb, rinv, T, D, eps); break;
+      case 7: hipLaunchKernelGGL(rmsnorm_fwd_vec_kernel<7>, g, b, 0, s, x, w, y, yb, rinv, T, D, eps); break;
+      default: hipLaunchKernelGGL(rmsnorm_fwd_vec_kernel<8>, g, b, 0, s, x, w, y, yb, rinv, T, D, eps); break;
+    }
+  } else {
+    hipLaunchKernelGGL(rmsnorm_fwd_kernel, g, b, 0, s, x, w, y, yb, rinv, T, D, eps);
+  }
   SMHIP_CHECK_LAUNCH();
   return SMHIP_OK;
 }

@@ -255,12 +255,14 @@ __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
     float o[E];
     if (neox) {
       const bool lo = l * E < P;
+      // the lane's E positions (l*E) % P .. +E-1 are consecutive: one vector load per table
+      float cs[E], sn[E];
+      ldE<E>(cosT + (int64_t)pos * P + (l * E) % P, cs);
+      ldE<E>(sinT + (int64_t)pos * P + (l * E) % P, sn);
 #pragma unroll
       for (int i = 0; i < E; i++) {
-        const int p = (l * E + i) % P;
-        const float c = cosT[(int64_t)pos * P + p], sn = sinT[(int64_t)pos * P + p];
         const float partner = __shfl_xor(v[i], 16, 64);
-        o[i] = lo ? v[i] * c - partner * sn : v[i] * c + partner * sn;
+        o[i] = lo ? v[i] * cs[i] - partner * sn[i] : v[i] * cs[i] + partner * sn[i];
       }
     } else {
 #pragma unroll
@@ -324,12 +326,13 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
     float gr[E];
     if (neox) {
       const bool lo = l * E < P;
+      float cs[E], sn[E];
+      ldE<E>(cosT + (int64_t)pos * P + (l * E) % P, cs);
+      ldE<E>(sinT + (int64_t)pos * P + (l * E) % P, sn);
 #pragma unroll
       for (int i = 0; i < E; i++) {
-        const int p = (l * E + i) % P;
-        const float c = cosT[(int64_t)pos * P + p], sn = sinT[(int64_t)pos * P + p];
         const float partner = __shfl_xor(g[i], 16, 64);
-        gr[i] = lo ? c * g[i] + sn * partner : -sn * partner + c * g[i];
+        gr[i] = lo ? cs[i] * g[i] + sn[i] * partner : -sn[i] * partner + cs[i] * g[i];
       }
     } else {
 #pragma unroll
@@ -472,17 +475,89 @@ __global__ __launch_bounds__(256) void swiglu_fused_bwd_kernel(const TD* __restr
   }
 }
 
+// 8 consecutive elements per thread (F % 8 == 0, 16-byte aligned rows): 16-byte loads and
+// stores for bf16, two float4 for fp32; the same per-element arithmetic as the scalar kernels
+__device__ inline void ld8(const uint16_t* p, float* f) {
+  const uint4 v = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    f[2 * i] = bf2f((uint16_t)(w[i] & 0xFFFFu));
+    f[2 * i + 1] = bf2f((uint16_t)(w[i] >> 16));
+  }
+}
+__device__ inline void ld8(const float* p, float* f) {
+  const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+  f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+__device__ inline void st8(uint16_t* p, const float* f) {
+  *reinterpret_cast<uint4*>(p) = make_uint4(pack_bf2(f[0], f[1]), pack_bf2(f[2], f[3]), pack_bf2(f[4], f[5]), pack_bf2(f[6], f[7]));
+}
+__device__ inline void st8(float* p, const float* f) {
+  *reinterpret_cast<float4*>(p) = make_float4(f[0], f[1], f[2], f[3]);
+  *reinterpret_cast<float4*>(p + 4) = make_float4(f[4], f[5], f[6], f[7]);
+}
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void swiglu_fused_fwd_vec_kernel(const TI* __restrict__ gu, TO* __restrict__ act, int T, int F) {
+  const int64_t n8 = (int64_t)T * F / 8;
+  for (int64_t i8 = (int64_t)blockIdx.x * 256 + threadIdx.x; i8 < n8; i8 += (int64_t)gridDim.x * 256) {
+    const int64_t i = i8 * 8, t = i / F, d = i - t * F;
+    float g[8], u[8], o[8];
+    ld8(gu + t * 2 * F + d, g);
+    ld8(gu + t * 2 * F + F + d, u);
+#pragma unroll
+    for (int k = 0; k < 8; k++) o[k] = (g[k] / (1.f + expf(-g[k]))) * u[k];
+    st8(act + i, o);
+  }
+}
+template <typename TD, typename TI, typename TO>
+__global__ __launch_bounds__(256) void swiglu_fused_bwd_vec_kernel(const TD* __restrict__ dA, const TI* __restrict__ gu,
+                                                                   TO* __restrict__ dgu, int T, int F) {
+  const int64_t n8 = (int64_t)T * F / 8;
+  for (int64_t i8 = (int64_t)blockIdx.x * 256 + threadIdx.x; i8 < n8; i8 += (int64_t)gridDim.x * 256) {
+    const int64_t i = i8 * 8, t = i / F, d = i - t * F;
+    float g[8], u[8], da[8], og[8], ou[8];
+    ld8(gu + t * 2 * F + d, g);
+    ld8(gu + t * 2 * F + F + d, u);
+    ld8(dA + i, da);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const float sig = 1.f / (1.f + expf(-g[k]));
+      ou[k] = da[k] * (g[k] * sig);
+      og[k] = da[k] * (sig * (1.f + g[k] * (1.f - sig))) * u[k];
+    }
+    st8(dgu + t * 2 * F + F + d, ou);
+    st8(dgu + t * 2 * F + d, og);
+  }
+}
+
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 int swiglu_fused_forward(const void* gu, void* act, int T, int F, int bf16, hipStream_t s) {
-  const int g = gridn((int64_t)T * F);
-  if (bf16) hipLaunchKernelGGL((swiglu_fused_fwd_kernel<uint16_t, uint16_t>), dim3(g), dim3(256), 0, s, (const uint16_t*)gu, (uint16_t*)act, T, F);
-  else hipLaunchKernelGGL((swiglu_fused_fwd_kernel<float, float>), dim3(g), dim3(256), 0, s, (const float*)gu, (float*)act, T, F);
+  const bool vec = F % 8 == 0 && al16(gu) && al16(act);
+  const int g = gridn((int64_t)T * F / (vec ? 8 : 1));
+  if (vec) {
+    if (bf16) hipLaunchKernelGGL((swiglu_fused_fwd_vec_kernel<uint16_t, uint16_t>), dim3(g), dim3(256), 0, s, (const uint16_t*)gu, (uint16_t*)act, T, F);
+    else hipLaunchKernelGGL((swiglu_fused_fwd_vec_kernel<float, float>), dim3(g), dim3(256), 0, s, (const float*)gu, (float*)act, T, F);
+  } else if (bf16) {
+    hipLaunchKernelGGL((swiglu_fused_fwd_kernel<uint16_t, uint16_t>), dim3(g), dim3(256), 0, s, (const uint16_t*)gu, (uint16_t*)act, T, F);
+  } else {
+    hipLaunchKernelGGL((swiglu_fused_fwd_kernel<float, float>), dim3(g), dim3(256), 0, s, (const float*)gu, (float*)act, T, F);
+  }
   SMHIP_CHECK_LAUNCH();
   return SMHIP_OK;
 }
 int swiglu_fused_backward(const void* dA, const void* gu, void* dgu, int T, int F, int bf16, hipStream_t s) {
-  const int g = gridn((int64_t)T * F);
-  if (bf16) hipLaunchKernelGGL((swiglu_fused_bwd_kernel<uint16_t, uint16_t, uint16_t>), dim3(g), dim3(256), 0, s, (const uint16_t*)dA, (const uint16_t*)gu, (uint16_t*)dgu, T, F);
-  else hipLaunchKernelGGL((swiglu_fused_bwd_kernel<float, float, float>), dim3(g), dim3(256), 0, s, (const float*)dA, (const float*)gu, (float*)dgu, T, F);
+  const bool vec = F % 8 == 0 && al16(dA) && al16(gu) && al16(dgu);
+  const int g = gridn((int64_t)T * F / (vec ? 8 : 1));
+  if (vec) {
+    if (bf16) hipLaunchKernelGGL((swiglu_fused_bwd_vec_kernel<uint16_t, uint16_t, uint16_t>), dim3(g), dim3(256), 0, s, (const uint16_t*)dA, (const uint16_t*)gu, (uint16_t*)dgu, T, F);
+    else hipLaunchKernelGGL((swiglu_fused_bwd_vec_kernel<float, float, float>), dim3(g), dim3(256), 0, s, (const float*)dA, (const float*)gu, (float*)dgu, T, F);
+  } else if (bf16) {
+    hipLaunchKernelGGL((swiglu_fused_bwd_kernel<uint16_t, uint16_t, uint16_t>), dim3(g), dim3(256), 0, s, (const uint16_t*)dA, (const uint16_t*)gu, (uint16_t*)dgu, T, F);
+  } else {
+    hipLaunchKernelGGL((swiglu_fused_bwd_kernel<float, float, float>), dim3(g), dim3(256), 0, s, (const float*)dA, (const float*)gu, (float*)dgu, T, F);
+  }
   SMHIP_CHECK_LAUNCH();
   return SMHIP_OK;
 }

@@ -244,6 +244,37 @@ __global__ __launch_bounds__(256) void fa_bwd_pre_kernel(const uint16_t* __restr
   }
 }
 
+// vectorised form: D/8 lanes per row, one 16-byte load of O and of dO per lane, the lane
+// products summed in d order and then over the lane group by xor shuffles
+template <int D>
+__global__ __launch_bounds__(256) void fa_bwd_pre_vec_kernel(const uint16_t* __restrict__ o, const uint16_t* __restrict__ dO,
+                                                             float* __restrict__ Di, int B, int S, int Hq, int64_t ldo,
+                                                             int64_t lddo) {
+  constexpr int L = D / 8;  // lanes per row
+  const int sub = threadIdx.x % L;
+  const int64_t rows = (int64_t)B * Hq * S;
+  for (int64_t r = ((int64_t)blockIdx.x * 256 + threadIdx.x) / L; r - ((int)threadIdx.x % 64) / L < rows;
+       r += (int64_t)gridDim.x * (256 / L)) {
+    const bool live = r < rows;
+    const int64_t rr = live ? r : rows - 1;
+    const int qi = (int)(rr % S);
+    const int h = (int)((rr / S) % Hq);
+    const int b = (int)(rr / ((int64_t)S * Hq));
+    const uint4 a = *reinterpret_cast<const uint4*>(o + ((int64_t)b * S + qi) * ldo + h * D + sub * 8);
+    const uint4 g = *reinterpret_cast<const uint4*>(dO + ((int64_t)b * S + qi) * lddo + h * D + sub * 8);
+    const uint32_t av[4] = {a.x, a.y, a.z, a.w}, gv[4] = {g.x, g.y, g.z, g.w};
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      acc += bf2f((uint16_t)(av[i] & 0xFFFFu)) * bf2f((uint16_t)(gv[i] & 0xFFFFu));
+      acc += bf2f((uint16_t)(av[i] >> 16)) * bf2f((uint16_t)(gv[i] >> 16));
+    }
+#pragma unroll
+    for (int m = 1; m < L; m <<= 1) acc += __shfl_xor(acc, m, 64);
+    if (live && sub == 0) Di[((int64_t)b * Hq + h) * S + qi] = acc;
+  }
+}
+
 // ============================================================================
 // backward dK, dV: grid (S/128, Hq, B); 4 waves x 32 keys; query tiles of QB = 64 (two
 // 32-query MFMA blocks per wave per tile).  Writes per-query-head partials dKh/dVh
@@ -528,12 +559,17 @@ int flash_backward(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
   float* dVh = dKh + (size_t)B * S * Hq * D;
   const int64_t rows = (int64_t)B * Hq * S;
   const int gpre = (int)std::min<int64_t>((rows + 3) / 4, (int64_t)num_cus() * 8);
+  const bool pre_vec = ((uintptr_t)o | (uintptr_t)dO) % 16 == 0 && ldo % 8 == 0 && lddo % 8 == 0;
+  const int gpre_v = (int)std::min<int64_t>((rows * (D / 8) + 255) / 256, (int64_t)num_cus() * 8);
   const int gred = (int)std::min<int64_t>(((int64_t)B * S * Hkv * D + 255) / 256, (int64_t)num_cus() * 8);
   const bool pair = (S / 128) % 2 == 0;
   const dim3 grid(pair ? S / 256 : S / 128, Hq, B), block(pair ? 512 : 256);
   const int ev0 = prof_mark(s);
 #define FA_BWD(DD, PP)                                                                                          \
-  hipLaunchKernelGGL(fa_bwd_pre_kernel<DD>, dim3(gpre), dim3(256), 0, s, o, dO, Di, B, S, Hq, ldo, lddo);      \
+  if (pre_vec)                                                                                                  \
+    hipLaunchKernelGGL(fa_bwd_pre_vec_kernel<DD>, dim3(gpre_v), dim3(256), 0, s, o, dO, Di, B, S, Hq, ldo, lddo); \
+  else                                                                                                          \
+    hipLaunchKernelGGL(fa_bwd_pre_kernel<DD>, dim3(gpre), dim3(256), 0, s, o, dO, Di, B, S, Hq, ldo, lddo);    \
   hipLaunchKernelGGL((fa_bwd_dkdv_kernel<DD, PP>), grid, block, 0, s, q, k, v, dO, lse, Di, dKh, dVh, S, Hq,   \
                      Hkv, ldq, ldk, ldv, lddo, sl2, scale);                                                     \
   hipLaunchKernelGGL((fa_bwd_dq_kernel<DD, PP>), grid, block, 0, s, q, k, v, dO, lse, Di, dq, S, Hq, Hkv, ldq, \
