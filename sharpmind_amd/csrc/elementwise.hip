@@ -58,6 +58,15 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_bwd_kernel(
     const float* xr = xin + (int64_t)t * D;
     const float ri = rinv[t];
     float yv[NCH][VEC], xv[NCH][VEC], wv_[NCH][VEC];
+    // the accumulate target is loaded with the inputs: one memory round trip per row
+    float4 prev[VEC == 4 ? NCH : 1];
+    if constexpr (VEC == 4) {
+#pragma unroll
+      for (int c = 0; c < NCH; c++) {
+        const int col = (c * 64 + lane) * VEC;
+        prev[c] = accumulate && col < D ? ld4(dX + (int64_t)t * D + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
     float dot = 0.f;
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
@@ -89,14 +98,25 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_bwd_kernel(
         for (int v = 0; v < VEC; v++) o[v] = ri * (yv[c][v] * wv_[c][v] - xv[c][v] * dot);
         float* dst = dX + (int64_t)t * D + col;
         if (accumulate) {
+          if constexpr (VEC == 4) {
+            o[0] = prev[c].x + o[0];
+            o[1] = prev[c].y + o[1];
+            o[2] = prev[c].z + o[2];
+            o[3] = prev[c].w + o[3];
+          } else {
 #pragma unroll
-          for (int v = 0; v < VEC; v++) o[v] = dst[v] + o[v];
+            for (int v = 0; v < VEC; v++) o[v] = dst[v] + o[v];
+          }
         }
         if constexpr (VEC == 4) st4(dst, make_float4(o[0], o[1], o[2], o[3]));
         else dst[0] = o[0];
         if (dX_bf16) {
+          if constexpr (VEC == 4) {
+            *reinterpret_cast<uint2*>(dX_bf16 + (int64_t)t * D + col) = make_uint2(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]));
+          } else {
 #pragma unroll
-          for (int v = 0; v < VEC; v++) dX_bf16[(int64_t)t * D + col + v] = f2bf(o[v]);
+            for (int v = 0; v < VEC; v++) dX_bf16[(int64_t)t * D + col + v] = f2bf(o[v]);
+          }
         }
       }
     }
@@ -178,7 +198,7 @@ static int rmsnorm_bwd_dispatch(const float* dY, const float* x, const float* ri
                                 float* dw, float* dX, int T, int D, int accumulate, uint16_t* dXb,
                                 hipStream_t s) {
   const bool v4 = (D % 4 == 0) && ((uintptr_t)dY % 16 == 0) && ((uintptr_t)x % 16 == 0) &&
-                  ((uintptr_t)w % 16 == 0) && ((uintptr_t)dX % 16 == 0);
+                  ((uintptr_t)w % 16 == 0) && ((uintptr_t)dX % 16 == 0) && ((uintptr_t)dXb % 8 == 0);
   if (v4) {
     int nch = ceil_div(D, 256);
     if (nch <= 1) return rmsnorm_bwd_launch<4, 1, FROM_X, HAS_DW>(dY, x, rinv, w, dw, dX, T, D, accumulate, dXb, s);
