@@ -621,20 +621,21 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
                         e->bf ? (uint16_t*)e->dh_ta : nullptr, s));
     // AttentionBackward (BackpropEngine.cs:539-602)
     R_(proj_backward(e, l, P_O, e->dh_ta, e->dh, sv.o, nullptr, e->bf, e->dO, s));
-    const float *dk = e->dk, *dv = e->dv;
+    const void *dk = e->dk, *dv = e->dv;
     int kv_grp = 0;
     if (e->bf) {
-      // dK / dV stay per query head; the QK-norm / RoPE backward sums each GQA group as it reads them
+      // dK / dV stay per query head; the QK-norm / RoPE backward sums each GQA group as it reads
+      // them.  dQ and the partials are bf16: their one consumer rounds its output to bf16.
       R_(flash_backward((const uint16_t*)sv.q, (const uint16_t*)sv.k, (const uint16_t*)sv.v, (const uint16_t*)sv.o,
                         (const uint16_t*)e->dO, sv.lse, e->dq, nullptr, nullptr, c.batch, c.seq, Hq, Hkv, D, e->qd,
-                        e->kvd, e->kvd, e->qd, e->qd, e->qd, e->kvd, e->kvd, e->flash_ws, s));
+                        e->kvd, e->kvd, e->qd, e->qd, e->qd, e->kvd, e->kvd, e->flash_ws, s, 1));
       flash_backward_partials(e->flash_ws, c.batch, c.seq, Hq, D, &dk, &dv);
       kv_grp = Hq / Hkv;
     } else {
       R_(attention_probs_backward((const float*)e->dO, (const float*)sv.q, (const float*)sv.k, (const float*)sv.v,
                                   sv.probs, e->dq, e->dk, e->dv, c.batch, c.seq, Hq, Hkv, D, s));
     }
-    R_(qkv_prep_backward(e->dq, dk, dv, sv.qkv, e->qkv_bf, sv.rinv_qk, c.qk_norm ? w.qn.data : nullptr,
+    R_(qkv_prep_backward(e->dq, dk, dv, e->bf, sv.qkv, e->qkv_bf, sv.rinv_qk, c.qk_norm ? w.qn.data : nullptr,
                          c.qk_norm ? w.kn.data : nullptr, c.qk_norm ? w.qn.grad : nullptr,
                          c.qk_norm ? w.kn.grad : nullptr, e->cosT, e->sinT, e->dqkv, T, c.seq, Hq, Hkv, D,
                          c.qk_norm, c.rope_neox, e->bf, kv_grp, s));

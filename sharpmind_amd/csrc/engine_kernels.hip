@@ -277,9 +277,9 @@ __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
   }
 }
 
-template <int D, typename TA, typename TQ>
+template <int D, typename TA, typename TQ, typename TG>
 __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
-    const float* __restrict__ dq, const float* __restrict__ dk, const float* __restrict__ dv,
+    const TG* __restrict__ dq, const TG* __restrict__ dk, const TG* __restrict__ dv,
     const TQ* __restrict__ qkv, const float* __restrict__ rinv, const float* __restrict__ wq,
     const float* __restrict__ wk, const float* __restrict__ cosT, const float* __restrict__ sinT,
     TA* __restrict__ dqkv, float* __restrict__ part, int T, int S, int Hq, int Hkv, int qk_norm, int neox,
@@ -288,12 +288,12 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
   const int l = threadIdx.x & 31, hw = threadIdx.x >> 5;  // half-wave 0..7
   // kv_grp > 0: dk / dv are the attention backward's per-query-head partials [T, Hq, D]; a KV
   // head's gradient is the sum of its kv_grp query heads, added in ascending head order
-  auto ld_kv = [&](const float* base, int t, int kvh, float* g) {
+  auto ld_kv = [&](const TG* base, int t, int kvh, float* g) {
     if (kv_grp == 0) {
       ldE<E>(base + (int64_t)t * Hkv * D + kvh * D + l * E, g);
       return;
     }
-    const float* p0 = base + ((int64_t)t * Hq + (int64_t)kvh * kv_grp) * D + l * E;
+    const TG* p0 = base + ((int64_t)t * Hq + (int64_t)kvh * kv_grp) * D + l * E;
     float h[E];
 #pragma unroll
     for (int i = 0; i < E; i++) g[i] = 0.f;
@@ -411,12 +411,14 @@ int qkv_prep_forward(const void* qkv, int qkv_bf16, void* q, void* k, void* v, f
   return SMHIP_OK;
 }
 
-int qkv_prep_backward(const float* dq, const float* dk, const float* dv, const void* qkv, int qkv_bf16,
+int qkv_prep_backward(const void* dq_, const void* dk_, const void* dv_, int grads_bf16, const void* qkv, int qkv_bf16,
                       const float* rinv,
                       const float* wq, const float* wk, float* dwq, float* dwk, const float* cosT,
                       const float* sinT, void* dqkv, int T, int S, int Hq, int Hkv, int D, int qk_norm,
                       int neox, int bf16, int kv_grp, hipStream_t s) {
   SMHIP_REQUIRE(D <= 128 && D % 2 == 0, "qkv prep: head_dim must be even and <= 128");
+  SMHIP_REQUIRE(!grads_bf16 || D == 128 || D == 64, "qkv prep: bf16 attention gradients need head_dim 64 or 128");
+  const float *dq = (const float*)dq_, *dk = (const float*)dk_, *dv = (const float*)dv_;
   SMHIP_REQUIRE(kv_grp == 0 || ((D == 128 || D == 64) && kv_grp * Hkv == Hq),
                 "qkv prep: per-query-head K/V partials need head_dim 64 or 128 and kv_grp = Hq / Hkv");
   const int64_t rows = (int64_t)T * (Hq + 2 * Hkv);
@@ -432,8 +434,14 @@ int qkv_prep_backward(const float* dq, const float* dk, const float* dv, const v
   SMHIP_REQUIRE(vec || !qkv_bf16, "qkv prep: bf16 projections need head_dim 64 or 128");
   SMHIP_REQUIRE(bf16 || !qkv_bf16, "qkv prep: bf16 projections need bf16 outputs");
   if (vec) {
-#define SMHIP_QKV_BWD(DD, TT, TQ) \
-  hipLaunchKernelGGL((qkv_prep_bwd_vec_kernel<DD, TT, TQ>), dim3(g), dim3(256), 0, s, dq, dk, dv, (const TQ*)qkv, rinv, wq, wk, cosT, sinT, (TT*)dqkv, part, T, S, Hq, Hkv, qk_norm, neox, kv_grp)
+#define SMHIP_QKV_BWD(DD, TT, TQ)                                                                                  \
+  if (grads_bf16)                                                                                                  \
+    hipLaunchKernelGGL((qkv_prep_bwd_vec_kernel<DD, TT, TQ, uint16_t>), dim3(g), dim3(256), 0, s,                  \
+                       (const uint16_t*)dq_, (const uint16_t*)dk_, (const uint16_t*)dv_, (const TQ*)qkv, rinv, wq, \
+                       wk, cosT, sinT, (TT*)dqkv, part, T, S, Hq, Hkv, qk_norm, neox, kv_grp);                     \
+  else                                                                                                             \
+    hipLaunchKernelGGL((qkv_prep_bwd_vec_kernel<DD, TT, TQ, float>), dim3(g), dim3(256), 0, s, dq, dk, dv,         \
+                       (const TQ*)qkv, rinv, wq, wk, cosT, sinT, (TT*)dqkv, part, T, S, Hq, Hkv, qk_norm, neox, kv_grp)
     if (qkv_bf16) { if (D == 128) SMHIP_QKV_BWD(128, uint16_t, uint16_t); else SMHIP_QKV_BWD(64, uint16_t, uint16_t); }
     else if (D == 128) { if (bf16) SMHIP_QKV_BWD(128, uint16_t, float); else SMHIP_QKV_BWD(128, float, float); }
     else { if (bf16) SMHIP_QKV_BWD(64, uint16_t, float); else SMHIP_QKV_BWD(64, float, float); }

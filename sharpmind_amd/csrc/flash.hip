@@ -36,6 +36,9 @@ __device__ inline void zero16(floatx16& a) {
   for (int e = 0; e < 16; e++) a[e] = 0.f;
 }
 __device__ inline bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
+// gradient outputs: fp32, or bf16 (the training engine, whose next consumer rounds to bf16)
+__device__ inline void stg(float* p, float v) { *p = v; }
+__device__ inline void stg(uint16_t* p, float v) { *p = f2bf(v); }
 // accumulator row of element e for this lane (32x32 MFMA output layout)
 __device__ inline int acc_row(int e, int lane) { return (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3); }
 
@@ -280,11 +283,11 @@ __global__ __launch_bounds__(256) void fa_bwd_pre_vec_kernel(const uint16_t* __r
 // 32-query MFMA blocks per wave per tile).  Writes per-query-head partials dKh/dVh
 // [B, S, Hq, D] fp32.
 // ============================================================================
-template <int D, bool PAIR>
+template <int D, bool PAIR, typename TG>
 __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_bwd_dkdv_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
-    float* __restrict__ dKh, float* __restrict__ dVh, int S, int Hq, int Hkv, int64_t ldq, int64_t ldk,
+    TG* __restrict__ dKh, TG* __restrict__ dVh, int S, int Hq, int Hkv, int64_t ldq, int64_t ldk,
     int64_t ldv, int64_t lddo, float sl2, float scale) {
   constexpr int QB = 64, NQ = QB / 32, RP = D + 8, TP = QB + 4, NT = PAIR ? 512 : 256;
   __shared__ __attribute__((aligned(16))) uint16_t sQ[QB * RP];
@@ -395,19 +398,19 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_bwd_dkdv_kernel(
     for (int e = 0; e < 16; e++) {
       const int key = kw0 + acc_row(e, lane);
       const int64_t off = (((int64_t)b * S + key) * Hq + h) * D + i * 32 + (lane & 31);
-      dKh[off] = dk[i][e] * scale;
-      dVh[off] = dv[i][e];
+      stg(dKh + off, dk[i][e] * scale);
+      stg(dVh + off, dv[i][e]);
     }
 }
 
 // ============================================================================
 // backward dQ: grid (S/128, Hq, B); 4 waves x 32 queries; key tiles of 64
 // ============================================================================
-template <int D, bool PAIR>
+template <int D, bool PAIR, typename TG>
 __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_bwd_dq_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
-    float* __restrict__ dq, int S, int Hq, int Hkv, int64_t ldq, int64_t ldk, int64_t ldv, int64_t lddo,
+    TG* __restrict__ dq, int S, int Hq, int Hkv, int64_t ldq, int64_t ldk, int64_t ldv, int64_t lddo,
     int64_t lddq, float sl2, float scale) {
   constexpr int KB = 64, RP = D + 8, TP = KB + 4, NT = PAIR ? 512 : 256;
   __shared__ __attribute__((aligned(16))) uint16_t sK[KB * RP];
@@ -481,14 +484,16 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_bwd_dq_kernel(
       for (int i = 0; i < D / 32; i++) acc[i] = mfma16(tload(sKt + (i * 32 + (lane & 31)) * TP, c * 16, lane), sf, acc[i]);
     }
   }
-  float* qrow = dq + ((int64_t)b * S + qi) * lddq + h * D;
+  TG* qrow = dq + ((int64_t)b * S + qi) * lddq + h * D;
 #pragma unroll
   for (int i = 0; i < D / 32; i++)
 #pragma unroll
     for (int g = 0; g < 4; g++) {
       const int d = i * 32 + g * 8 + (lane >> 5) * 4;
-      *reinterpret_cast<float4*>(qrow + d) = make_float4(acc[i][4 * g] * scale, acc[i][4 * g + 1] * scale,
-                                                         acc[i][4 * g + 2] * scale, acc[i][4 * g + 3] * scale);
+      const float a0 = acc[i][4 * g] * scale, a1 = acc[i][4 * g + 1] * scale, a2 = acc[i][4 * g + 2] * scale,
+                  a3 = acc[i][4 * g + 3] * scale;
+      if constexpr (sizeof(TG) == 4) *reinterpret_cast<float4*>(qrow + d) = make_float4(a0, a1, a2, a3);
+      else *reinterpret_cast<uint2*>(qrow + d) = make_uint2(pack_bf2(a0, a1), pack_bf2(a2, a3));
     }
 }
 
@@ -540,23 +545,27 @@ size_t flash_backward_workspace(int B, int S, int Hq, int D) {
   return sizeof(float) * ((size_t)B * Hq * S + 2 * (size_t)B * S * Hq * D) + 256;
 }
 
-void flash_backward_partials(void* ws, int B, int S, int Hq, int D, const float** dKh, const float** dVh) {
+void flash_backward_partials(void* ws, int B, int S, int Hq, int D, const void** dKh, const void** dVh) {
   const float* Di = (const float*)ws;
-  *dKh = Di + (size_t)B * Hq * S;
-  *dVh = *dKh + (size_t)B * S * Hq * D;
+  const float* k = Di + (size_t)B * Hq * S;
+  *dKh = k;
+  *dVh = k + (size_t)B * S * Hq * D;
 }
 
 int flash_backward(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
-                   const uint16_t* dO, const float* lse, float* dq, float* dk, float* dv, int B, int S,
+                   const uint16_t* dO, const float* lse, void* dq, float* dk, float* dv, int B, int S,
                    int Hq, int Hkv, int D, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, int64_t lddo,
-                   int64_t lddq, int64_t lddk, int64_t lddv, void* ws, hipStream_t s) {
+                   int64_t lddq, int64_t lddk, int64_t lddv, void* ws, hipStream_t s, int bf16_grads) {
   SMHIP_REQUIRE(S % 128 == 0, "flash attention: S must be a multiple of 128");
   SMHIP_REQUIRE(Hkv > 0 && Hq % Hkv == 0, "flash attention: Hq must be a multiple of Hkv");
   SMHIP_REQUIRE((dk == nullptr) == (dv == nullptr), "flash attention backward: dk and dv are both given or both null");
+  SMHIP_REQUIRE(!bf16_grads || !dk, "flash attention backward: bf16 gradients leave dK/dV as per-head partials");
   const float scale = 1.f / sqrtf((float)D), sl2 = kLog2e * scale;
   float* Di = (float*)ws;
   float* dKh = Di + (size_t)B * Hq * S;
   float* dVh = dKh + (size_t)B * S * Hq * D;
+  uint16_t* dKb = (uint16_t*)dKh;  // bf16 partials use the first half of each region
+  uint16_t* dVb = (uint16_t*)dVh;
   const int64_t rows = (int64_t)B * Hq * S;
   const int gpre = (int)std::min<int64_t>((rows + 3) / 4, (int64_t)num_cus() * 8);
   const bool pre_vec = ((uintptr_t)o | (uintptr_t)dO) % 16 == 0 && ldo % 8 == 0 && lddo % 8 == 0;
@@ -570,10 +579,17 @@ int flash_backward(const uint16_t* q, const uint16_t* k, const uint16_t* v, cons
     hipLaunchKernelGGL(fa_bwd_pre_vec_kernel<DD>, dim3(gpre_v), dim3(256), 0, s, o, dO, Di, B, S, Hq, ldo, lddo); \
   else                                                                                                          \
     hipLaunchKernelGGL(fa_bwd_pre_kernel<DD>, dim3(gpre), dim3(256), 0, s, o, dO, Di, B, S, Hq, ldo, lddo);    \
-  hipLaunchKernelGGL((fa_bwd_dkdv_kernel<DD, PP>), grid, block, 0, s, q, k, v, dO, lse, Di, dKh, dVh, S, Hq,   \
-                     Hkv, ldq, ldk, ldv, lddo, sl2, scale);                                                     \
-  hipLaunchKernelGGL((fa_bwd_dq_kernel<DD, PP>), grid, block, 0, s, q, k, v, dO, lse, Di, dq, S, Hq, Hkv, ldq, \
-                     ldk, ldv, lddo, lddq, sl2, scale);                                                         \
+  if (bf16_grads) {                                                                                             \
+    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<DD, PP, uint16_t>), grid, block, 0, s, q, k, v, dO, lse, Di, dKb, dVb, \
+                       S, Hq, Hkv, ldq, ldk, ldv, lddo, sl2, scale);                                              \
+    hipLaunchKernelGGL((fa_bwd_dq_kernel<DD, PP, uint16_t>), grid, block, 0, s, q, k, v, dO, lse, Di,             \
+                       (uint16_t*)dq, S, Hq, Hkv, ldq, ldk, ldv, lddo, lddq, sl2, scale);                         \
+  } else {                                                                                                      \
+    hipLaunchKernelGGL((fa_bwd_dkdv_kernel<DD, PP, float>), grid, block, 0, s, q, k, v, dO, lse, Di, dKh, dVh,    \
+                       S, Hq, Hkv, ldq, ldk, ldv, lddo, sl2, scale);                                              \
+    hipLaunchKernelGGL((fa_bwd_dq_kernel<DD, PP, float>), grid, block, 0, s, q, k, v, dO, lse, Di, (float*)dq,    \
+                       S, Hq, Hkv, ldq, ldk, ldv, lddo, lddq, sl2, scale);                                        \
+  }                                                                                                             \
   if (dk)                                                                                                       \
     hipLaunchKernelGGL(fa_group_reduce_kernel<DD>, dim3(gred), dim3(256), 0, s, dKh, dVh, dk, dv, B, S, Hq, Hkv, \
                        lddk, lddv);

@@ -96,12 +96,13 @@ int flash_forward(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint1
                   hipStream_t s);
 size_t flash_backward_workspace(int B, int S, int Hq, int D);
 // dk == dv == nullptr: flash_backward leaves the per-query-head partials dK_h, dV_h [B*S, Hq, D]
-// (fp32) in the workspace instead of summing each GQA group; these are their addresses
-void flash_backward_partials(void* ws, int B, int S, int Hq, int D, const float** dKh, const float** dVh);
+// in the workspace instead of summing each GQA group; these are their addresses.  bf16_grads:
+// dq and the partials are bf16 (requires dk == dv == nullptr), fp32 otherwise.
+void flash_backward_partials(void* ws, int B, int S, int Hq, int D, const void** dKh, const void** dVh);
 int flash_backward(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o,
-                   const uint16_t* dO, const float* lse, float* dq, float* dk, float* dv, int B, int S,
+                   const uint16_t* dO, const float* lse, void* dq, float* dk, float* dv, int B, int S,
                    int Hq, int Hkv, int D, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo, int64_t lddo,
-                   int64_t lddq, int64_t lddk, int64_t lddv, void* ws, hipStream_t s);
+                   int64_t lddq, int64_t lddk, int64_t lddv, void* ws, hipStream_t s, int bf16_grads = 0);
 // attention.hip (probability-materialising path, head-strided)
 int attention_probs_backward(const float* dO, const float* q, const float* k, const float* v,
                              const float* probs, float* dq, float* dk, float* dv, int B, int S, int Hq,
@@ -110,7 +111,7 @@ int attention_probs_backward(const float* dO, const float* q, const float* k, co
 int qkv_prep_forward(const void* qkv, int qkv_bf16, void* q, void* k, void* v, float* rinv, const float* wq,
                      const float* wk, const float* cosT, const float* sinT, int T, int S, int Hq, int Hkv,
                      int D, int qk_norm, int neox, float eps, int bf16, hipStream_t s);
-int qkv_prep_backward(const float* dq, const float* dk, const float* dv, const void* qkv, int qkv_bf16,
+int qkv_prep_backward(const void* dq, const void* dk, const void* dv, int grads_bf16, const void* qkv, int qkv_bf16,
                       const float* rinv,
                       const float* wq, const float* wk, float* dwq, float* dwk, const float* cosT,
                       const float* sinT, void* dqkv, int T, int S, int Hq, int Hkv, int D, int qk_norm,
