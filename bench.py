@@ -7,9 +7,10 @@ Prints ONE JSON line.  The timed region is K full training steps (forward,
 backward, global-norm clip, AdamW) of the resident engine, bracketed by
 torch.cuda.synchronize().  Inputs (synthetic uniform token ids, next-token
 labels) are already in HBM.  The step runs as a replayed HIP graph (bit-identical
-to eager launches).  The dominant kernel's roofline comes from HIP events recorded
-by the library around each MFMA GEMM launch on its own stream during a separate
-pass of eager steps after the timed region (smhip_profile_begin/end).  cpu_baseline times the
+to eager launches).  The dominant kernel's roofline comes from HIP events the library
+records for each MFMA GEMM launch on its own stream (timestamped by the dispatch, via
+hipExtLaunchKernelGGL) during a separate pass of eager steps after the timed region
+(smhip_profile_begin/end).  cpu_baseline times the
 oracle's scalar C restatement of the same step on a bounded sample (see
 cpu_baseline()).
 """

@@ -250,7 +250,8 @@ int smhip_gguf_tensor_info(const char* path, int64_t index, char* name, int64_t 
  * dLogits after a fp32-mode backward).  Element type is bf16 for "xn1|q|k|v|o|gu|act" (and "qkv" with
  * head_dim 64 or 128) in bf16 mode, fp32 otherwise. */
 int smhip_engine_read_activation(void* engine, const char* what, int layer, void* host, int64_t nbytes);
-/* Live kernel timing on the calling thread: between begin and end, the GEMM and flash-attention
+/* Live kernel timing on the calling thread: between begin and end, the GEMM launcher times its main
+ * kernel with start/end events taken by the dispatch (hipExtLaunchKernelGGL) and the flash-attention
  * launchers bracket their kernels with HIP events on the launch stream.  end synchronises and writes
  * out[3*c + {0,1,2}] = (milliseconds, launches, algorithmic flops) for category c
  * (0 = MFMA GEMM kernel, 1 = flash forward, 2 = flash backward kernels, 3 = MFMA GEMM kernel with a

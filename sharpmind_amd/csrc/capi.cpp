@@ -81,6 +81,15 @@ int prof_mark(hipStream_t s) {
   return (int)p->used++;
 }
 bool profiling_active() { return g_prof != nullptr; }
+bool prof_reserve(int* i0, int* i1, hipEvent_t* e0, hipEvent_t* e1) {
+  Profiler* p = g_prof;
+  if (!p || p->used + 2 > p->ev.size()) return false;
+  *i0 = (int)p->used;
+  *e0 = p->ev[p->used++];
+  *i1 = (int)p->used;
+  *e1 = p->ev[p->used++];
+  return true;
+}
 void prof_add(int cat, int i0, int i1, double flops, int M, int N, int K) {
   if (g_prof && i0 >= 0 && i1 >= 0) g_prof->recs.push_back({cat, i0, i1, flops, M, N, K});
 }

@@ -174,6 +174,9 @@ int gemm(const GemmArgs& g, hipStream_t s);
 // quantised base as column planes, or tagged by the caller), counted apart from PROF_GEMM
 enum ProfCat { PROF_GEMM = 0, PROF_FLASH_FWD = 1, PROF_FLASH_BWD = 2, PROF_GEMM_DX = 3, PROF_NCAT = 4 };
 int prof_mark(hipStream_t s);                         // -1 when profiling is off
+// two unrecorded events (indices *i0, *i1) for a launch that timestamps its own start and end
+// (hipExtLaunchKernelGGL); false when profiling is off
+bool prof_reserve(int* i0, int* i1, hipEvent_t* e0, hipEvent_t* e1);
 bool profiling_active();
 void prof_add(int cat, int i0, int i1, double flops, int M = 0, int N = 0, int K = 0);
 
