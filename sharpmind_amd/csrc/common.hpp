@@ -164,6 +164,11 @@ struct GemmArgs {
   int64_t ldr;
   int prof_cat;        // live-timing category (0: by operand kind)
   struct SkinnyBatch* defer;  // rank-sized products: queue the split reduction here (see skinny_flush)
+  // block-diagonal mask of a fused LoRA B gradient, applied by the rank-sized (transposed) path;
+  // *masked is set to 1 when it was applied (0: the caller masks afterwards)
+  const int* mask_cols;
+  int mask_rank, mask_nblk;
+  int* masked;
 };
 int gemm(const GemmArgs& g, hipStream_t s);
 

@@ -85,6 +85,7 @@ struct Engine {
   bool base_ws = false;
   uint16_t *emb_b = nullptr, *emb_bt = nullptr;
   SkinnyBatch skb;                // deferred split reductions of a layer's adapter gradients
+  int lb_masked[4] = {};          // the last dB product of projection p applied the block-diagonal mask
   DequantJob* dq_jobs = nullptr;  // device table of the per-step decode (one launch)
   int dq_njobs = 0;
   int64_t dq_tiles = 0;
@@ -481,6 +482,12 @@ static int proj_backward(Engine* e, int l, int p, const void* dY, const float* d
     gb.C = w.lb[p].grad; gb.ldc = Out;
     gb.split_k = split_arg(e, nr, Out, T);
     gb.defer = &e->skb;
+    if (e->nblk[p] > 1) {  // fused q|k|v or gate|up: only the diagonal blocks of dB are gradients
+      gb.mask_cols = p == P_QKV ? w.lb_cols : w.lb_cols + 3;
+      gb.mask_rank = e->c.lora_rank;
+      gb.mask_nblk = e->nblk[p];
+      gb.masked = &e->lb_masked[p];
+    }
     if (int rc = gemm(gb, s)) return rc;
     // dA += s x^T z   [In, nr]
     GemmArgs ga{};
@@ -647,8 +654,9 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
       // of the fused B gradients back to zero
       R_(skinny_flush(&e->skb, s));
       const int nrq = e->nr[P_QKV], nrg = e->nr[P_GU];
-      R_(lora_mask(w.lb[P_QKV].grad, nrq, c.lora_rank, e->Out[P_QKV], w.lb_cols, 3, s));
-      R_(lora_mask(w.lb[P_GU].grad, nrg, c.lora_rank, e->Out[P_GU], w.lb_cols + 3, 2, s));
+      // (skipped where the rank-sized dB product already left those blocks untouched)
+      if (!e->lb_masked[P_QKV]) R_(lora_mask(w.lb[P_QKV].grad, nrq, c.lora_rank, e->Out[P_QKV], w.lb_cols, 3, s));
+      if (!e->lb_masked[P_GU]) R_(lora_mask(w.lb[P_GU].grad, nrg, c.lora_rank, e->Out[P_GU], w.lb_cols + 3, 2, s));
     }
   }
   if (!e->lora) R_(embedding_backward(e->dh, ids, e->emb.grad, T, d, V, s));  // BackpropEngine.cs:203-205

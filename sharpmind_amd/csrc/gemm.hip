@@ -395,6 +395,7 @@ static OpDev make_op(const Operand& o, int R, int K, float mult) {
 }
 
 int gemm(const GemmArgs& g, hipStream_t s) {
+  if (g.masked) *g.masked = 0;  // set by the rank-sized path when it applies the mask
   if (g.M <= 0 || g.N <= 0) return SMHIP_OK;
   if (!g.R || !g.c_bf16) {
     const int fast = gemm_bf16_fast(g, s);

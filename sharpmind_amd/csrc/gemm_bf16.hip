@@ -840,7 +840,9 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
         ? gemm_skinny(g.M, g.N, g.K, g.A.p, g.A.ld, am == SRC_BF16_K, g.B.p, g.B.ld, bm == SRC_BF16_K, g.alpha,
                       g.beta, g.C, g.ldc, false, g.c_bf16 != 0, g.defer, s)
         : gemm_skinny(g.N, g.M, g.K, g.B.p, g.B.ld, bm == SRC_BF16_K, g.A.p, g.A.ld, am == SRC_BF16_K, g.alpha,
-                      g.beta, g.C, g.ldc, true, g.c_bf16 != 0, g.defer, s);
+                      g.beta, g.C, g.ldc, true, g.c_bf16 != 0, g.defer, s,
+                      SkinnyMask{g.mask_cols, g.mask_rank, g.mask_nblk});
+    if (r > 0 && g.M <= 64 && g.N > 64 && g.mask_cols && g.masked) *g.masked = 1;
     if (r != 0) return r;
   }
   if (am == SRC_BF16_R && bm != SRC_BF16_R) return 0;

@@ -43,6 +43,13 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s);
 // partials into the batch's arena and queues the reduction; skinny_flush reduces everything
 // queued in one launch (also called by gemm_skinny when the arena or the queue is full).
 // Products whose result is not read before the flush (gradient accumulations) may be deferred.
+// Block-diagonal output mask of a fused LoRA B gradient (dB^T stored transposed, rows r of n,
+// columns m of M): entry (r, m) is written only when cols[r / rank] <= m < cols[r / rank + 1]
+// (M for the last block); the others keep their value (zero: gradients are cleared per step).
+struct SkinnyMask {
+  const int* cols = nullptr;  // device, nblk column starts; nullptr: no mask
+  int rank = 0, nblk = 0;
+};
 struct SkinnyJob {
   const float* partial;
   void* C;
@@ -50,6 +57,7 @@ struct SkinnyJob {
   int S, M, n;
   float alpha, beta;
   int trans, c_bf16;
+  SkinnyMask mask;
 };
 struct SkinnyBatch {
   static constexpr int kMaxJobs = 8;
@@ -61,7 +69,7 @@ struct SkinnyBatch {
 int skinny_flush(SkinnyBatch* b, hipStream_t s);
 int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, const void* small, int64_t lds,
                 bool small_k, float alpha, float beta, void* C, int64_t ldc, bool trans_out, bool c_bf16,
-                SkinnyBatch* defer, hipStream_t s);
+                SkinnyBatch* defer, hipStream_t s, SkinnyMask mask = SkinnyMask{});
 
 // quant.hip
 int dequant_raw(int qtype, const void* raw, float* out, int64_t n, hipStream_t s);

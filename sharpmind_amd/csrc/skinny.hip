@@ -47,11 +47,19 @@ struct Args {
   int M, n, K;
   int kps;          // k tiles per split
   float* partial;   // [S][M][n] when S > 1
+  SkinnyMask mask;  // block-diagonal output mask (transposed outputs of fused LoRA B gradients)
   void* C;
   int64_t ldc;
   float alpha, beta;
 };
 
+// entry (r, m) of the output is stored unless the block-diagonal mask excludes it
+__device__ __forceinline__ bool mask_keep(const SkinnyMask& mk, int r, int64_t m, int M) {
+  if (!mk.cols) return true;
+  const int blk = r / mk.rank;
+  const int lo = mk.cols[blk], hi = blk + 1 < mk.nblk ? mk.cols[blk + 1] : M;
+  return m >= lo && m < hi;
+}
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
 }
@@ -236,6 +244,7 @@ __global__ __launch_bounds__(256, 2) void skinny_kernel(Args a) {
           a.partial[((int64_t)split * a.M + row) * a.n + col] = acc[i][j][e];
           continue;
         }
+        if (!mask_keep(a.mask, col, row, a.M)) continue;
         const int64_t ci = TRANS_OUT ? (int64_t)col * a.ldc + row : (int64_t)row * a.ldc + col;
         float o = a.alpha * acc[i][j][e];
         if constexpr (C_BF16) {
@@ -257,7 +266,8 @@ __global__ __launch_bounds__(256, 2) void skinny_kernel(Args a) {
 // together.
 template <bool TRANS_OUT, bool C_BF16>
 __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restrict__ partial, int S, int M, int n,
-                                                            void* C, int64_t ldc, float alpha, float beta) {
+                                                            void* C, int64_t ldc, float alpha, float beta,
+                                                            SkinnyMask mask) {
   const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // float4 index
   const int64_t total = (int64_t)M * n / 4;
   if (q >= total) return;
@@ -286,6 +296,7 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
   const float v[4] = {acc[0], acc[1], acc[2], acc[3]};
 #pragma unroll
   for (int j = 0; j < 4; j++) {
+    if (!mask_keep(mask, r + j, m, M)) continue;
     const int64_t ci = TRANS_OUT ? (int64_t)(r + j) * ldc + m : m * ldc + r + j;
     float o = alpha * v[j];
     if constexpr (C_BF16) {
@@ -325,6 +336,7 @@ __global__ __launch_bounds__(256) void skinny_reduce_batch_kernel(BatchArgs b) {
   const float v[4] = {acc[0], acc[1], acc[2], acc[3]};
 #pragma unroll
   for (int e = 0; e < 4; e++) {
+    if (!mask_keep(j.mask, r + e, m, j.M)) continue;
     const int64_t ci = j.trans ? (int64_t)(r + e) * j.ldc + m : m * j.ldc + r + e;
     float o = j.alpha * v[e];
     if (j.c_bf16) {
@@ -383,7 +395,7 @@ int skinny_flush(SkinnyBatch* b, hipStream_t s) {
 
 int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, const void* small, int64_t lds,
                 bool small_k, float alpha, float beta, void* C, int64_t ldc, bool trans_out, bool c_bf16,
-                SkinnyBatch* defer, hipStream_t s) {
+                SkinnyBatch* defer, hipStream_t s, SkinnyMask mask) {
   using namespace sk;
   if (n < 1 || n > 64 || n % 16 || M < 1 || K < BKT || K % BKT) return 0;
   if (((uintptr_t)big | (uintptr_t)small) % 16 || ldb % 8) return 0;
@@ -399,6 +411,7 @@ int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, c
   a.small = small; a.lds = lds; a.small_bytes = (int)sb;
   a.M = M; a.n = n; a.K = K;
   a.C = C; a.ldc = ldc; a.alpha = alpha; a.beta = beta;
+  a.mask = mask;
   const int mt = ceil_div(M, MT), nk = K / BKT;
   // splits: two workgroups per CU; fewer while the fp32 partials (written and read back)
   // exceed a quarter of the bytes of Big, as long as every CU keeps a workgroup
@@ -415,7 +428,7 @@ int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, c
     if (defer->n == SkinnyBatch::kMaxJobs || defer->used + pbytes > defer->cap)
       if (int rc = skinny_flush(defer, s)) return rc;
     a.partial = (float*)((char*)defer->arena + defer->used);
-    defer->job[defer->n++] = SkinnyJob{a.partial, C, ldc, S, M, n, alpha, beta, trans_out ? 1 : 0, c_bf16 ? 1 : 0};
+    defer->job[defer->n++] = SkinnyJob{a.partial, C, ldc, S, M, n, alpha, beta, trans_out ? 1 : 0, c_bf16 ? 1 : 0, mask};
     defer->used += pbytes;
   } else if (S > 1) {
     a.partial = (float*)workspace(s, sizeof(float) * (size_t)S * M * n, 7);
@@ -432,11 +445,11 @@ int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, c
   if (S > 1 && !deferred) {
     const int blocks = ceil_div((int64_t)M * n / 4, 256);
     if (trans_out) {
-      if (c_bf16) hipLaunchKernelGGL((skinny_reduce_kernel<true, true>), dim3(blocks), dim3(256), 0, s, a.partial, S, M, n, C, ldc, alpha, beta);
-      else hipLaunchKernelGGL((skinny_reduce_kernel<true, false>), dim3(blocks), dim3(256), 0, s, a.partial, S, M, n, C, ldc, alpha, beta);
+      if (c_bf16) hipLaunchKernelGGL((skinny_reduce_kernel<true, true>), dim3(blocks), dim3(256), 0, s, a.partial, S, M, n, C, ldc, alpha, beta, mask);
+      else hipLaunchKernelGGL((skinny_reduce_kernel<true, false>), dim3(blocks), dim3(256), 0, s, a.partial, S, M, n, C, ldc, alpha, beta, mask);
     } else {
-      if (c_bf16) hipLaunchKernelGGL((skinny_reduce_kernel<false, true>), dim3(blocks), dim3(256), 0, s, a.partial, S, M, n, C, ldc, alpha, beta);
-      else hipLaunchKernelGGL((skinny_reduce_kernel<false, false>), dim3(blocks), dim3(256), 0, s, a.partial, S, M, n, C, ldc, alpha, beta);
+      if (c_bf16) hipLaunchKernelGGL((skinny_reduce_kernel<false, true>), dim3(blocks), dim3(256), 0, s, a.partial, S, M, n, C, ldc, alpha, beta, mask);
+      else hipLaunchKernelGGL((skinny_reduce_kernel<false, false>), dim3(blocks), dim3(256), 0, s, a.partial, S, M, n, C, ldc, alpha, beta, mask);
     }
     SMHIP_CHECK_LAUNCH();
   }
