@@ -220,60 +220,69 @@ __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
     float* __restrict__ rinv, const float* __restrict__ wq, const float* __restrict__ wk,
     const float* __restrict__ cosT, const float* __restrict__ sinT, int T, int S, int Hq, int Hkv,
     int qk_norm, int neox, float eps) {
-  constexpr int E = D / 32, P = D / 2;
-  const int l = threadIdx.x & 31;
+  constexpr int E = D / 32, P = D / 2, R = 4;  // R rows in flight per half-wave
+  const int l = threadIdx.x & 31, hw = threadIdx.x >> 5;
   const int H = Hq + 2 * Hkv, nqkv = H * D;
-  const int64_t rows = (int64_t)T * H;
-  const int64_t r0 = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
-  // every lane of a half-wave shares the row; both halves of a wave stay in the loop
-  // together (trip counts differ by at most one, handled by the row guard)
-  for (int64_t r = r0; r - (threadIdx.x >> 5 & 1) < rows; r += (int64_t)gridDim.x * 8) {
-    const bool live = r < rows;
-    const int64_t rr = live ? r : rows - 1;
-    const int t = (int)(rr / H), hh = (int)(rr % H);
-    const TQ* x = qkv + (int64_t)t * nqkv + hh * D + l * E;
-    float v[E];
-    ldE<E>(x, v);
-    if (hh >= Hq + Hkv) {
-      if (live) stE<E>(vo + (int64_t)t * Hkv * D + (hh - Hq - Hkv) * D + l * E, v);
-      continue;
-    }
-    const bool isq = hh < Hq;
-    const float* w = (isq ? wq : wk) + l * E;
-    float ri = 1.f;
-    if (qk_norm) {
-      float ss = 0.f;
-#pragma unroll
-      for (int i = 0; i < E; i++) ss += v[i] * v[i];
-      ss = half_sum(ss);
-      ri = 1.f / sqrtf(ss / (float)D + eps);
-      if (live && l == 0) rinv[(int64_t)t * (Hq + Hkv) + hh] = ri;
-#pragma unroll
-      for (int i = 0; i < E; i++) v[i] = v[i] * ri * w[i];
-    }
+  // workgroup per token: the half-waves take heads hw, hw + 8, ...; the lane's RoPE factors
+  // depend only on the lane and the position, so they are loaded once per token
+  for (int t = blockIdx.x; t < T; t += gridDim.x) {
     const int pos = t % S;
-    float o[E];
+    float cs[E], sn[E];
     if (neox) {
-      const bool lo = l * E < P;
-      // the lane's E positions (l*E) % P .. +E-1 are consecutive: one vector load per table
-      float cs[E], sn[E];
       ldE<E>(cosT + (int64_t)pos * P + (l * E) % P, cs);
       ldE<E>(sinT + (int64_t)pos * P + (l * E) % P, sn);
-#pragma unroll
-      for (int i = 0; i < E; i++) {
-        const float partner = __shfl_xor(v[i], 16, 64);
-        o[i] = lo ? v[i] * cs[i] - partner * sn[i] : v[i] * cs[i] + partner * sn[i];
-      }
     } else {
 #pragma unroll
       for (int i = 0; i < E; i += 2) {
         const int p = (l * E + i) / 2;
-        const float c = cosT[(int64_t)pos * P + p], sn = sinT[(int64_t)pos * P + p];
-        o[i] = v[i] * c - v[i + 1] * sn;
-        o[i + 1] = v[i + 1] * c + v[i] * sn;
+        cs[i] = cs[i + 1] = cosT[(int64_t)pos * P + p];
+        sn[i] = sn[i + 1] = sinT[(int64_t)pos * P + p];
       }
     }
-    if (live) stE<E>((isq ? qo + (int64_t)t * Hq * D + hh * D : ko + (int64_t)t * Hkv * D + (hh - Hq) * D) + l * E, o);
+    const TQ* xt = qkv + (int64_t)t * nqkv;
+    for (int h0 = hw; h0 < H; h0 += 8 * R) {
+      float v[R][E];
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        if (h0 + 8 * r < H) ldE<E>(xt + (h0 + 8 * r) * D + l * E, v[r]);
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const int hh = h0 + 8 * r;
+        if (hh >= H) break;
+        if (hh >= Hq + Hkv) {
+          stE<E>(vo + (int64_t)t * Hkv * D + (hh - Hq - Hkv) * D + l * E, v[r]);
+          continue;
+        }
+        const bool isq = hh < Hq;
+        const float* w = (isq ? wq : wk) + l * E;
+        if (qk_norm) {
+          float ss = 0.f;
+#pragma unroll
+          for (int i = 0; i < E; i++) ss += v[r][i] * v[r][i];
+          ss = half_sum(ss);
+          const float ri = 1.f / sqrtf(ss / (float)D + eps);
+          if (l == 0) rinv[(int64_t)t * (Hq + Hkv) + hh] = ri;
+#pragma unroll
+          for (int i = 0; i < E; i++) v[r][i] = v[r][i] * ri * w[i];
+        }
+        float o[E];
+        if (neox) {
+          const bool lo = l * E < P;
+#pragma unroll
+          for (int i = 0; i < E; i++) {
+            const float partner = __shfl_xor(v[r][i], 16, 64);
+            o[i] = lo ? v[r][i] * cs[i] - partner * sn[i] : v[r][i] * cs[i] + partner * sn[i];
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < E; i += 2) {
+            o[i] = v[r][i] * cs[i] - v[r][i + 1] * sn[i];
+            o[i + 1] = v[r][i + 1] * cs[i] + v[r][i] * sn[i];
+          }
+        }
+        stE<E>((isq ? qo + (int64_t)t * Hq * D + hh * D : ko + (int64_t)t * Hkv * D + (hh - Hq) * D) + l * E, o);
+      }
+    }
   }
 }
 
@@ -297,6 +306,14 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
     float h[E];
 #pragma unroll
     for (int i = 0; i < E; i++) g[i] = 0.f;
+    if (kv_grp == 2) {  // both loads in flight before the (ordered) adds
+      float h1[E];
+      ldE<E>(p0, h);
+      ldE<E>(p0 + D, h1);
+#pragma unroll
+      for (int i = 0; i < E; i++) g[i] = (g[i] + h[i]) + h1[i];
+      return;
+    }
     for (int j = 0; j < kv_grp; j++) {
       ldE<E>(p0 + (int64_t)j * D, h);
 #pragma unroll
@@ -304,68 +321,87 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
     }
   };
   const int H = Hq + 2 * Hkv, nqkv = H * D;
-  const int64_t rows = (int64_t)T * H;
+  constexpr int R = 2;  // rows in flight per half-wave (4 costs occupancy: 135 registers)
   float aq[E], ak[E];
 #pragma unroll
   for (int i = 0; i < E; i++) { aq[i] = 0.f; ak[i] = 0.f; }
-  for (int64_t r = (int64_t)blockIdx.x * 8 + hw; r - (hw & 1) < rows; r += (int64_t)gridDim.x * 8) {
-    const bool live = r < rows;
-    const int64_t rr = live ? r : rows - 1;
-    const int t = (int)(rr / H), hh = (int)(rr % H);
-    TA* dst = dqkv + (int64_t)t * nqkv + hh * D + l * E;
-    float g[E];
-    if (hh >= Hq + Hkv) {
-      ld_kv(dv, t, hh - Hq - Hkv, g);
-      if (live) stE<E>(dst, g);
-      continue;
-    }
-    const bool isq = hh < Hq;
-    if (isq) ldE<E>(dq + (int64_t)t * Hq * D + hh * D + l * E, g);
-    else ld_kv(dk, t, hh - Hq, g);
+  // workgroup per token: the half-waves take heads hw, hw + 8, ...; RoPE factors once per token
+  for (int t = blockIdx.x; t < T; t += gridDim.x) {
     const int pos = t % S;
-    float gr[E];
+    float cs[E], sn[E];
     if (neox) {
-      const bool lo = l * E < P;
-      float cs[E], sn[E];
       ldE<E>(cosT + (int64_t)pos * P + (l * E) % P, cs);
       ldE<E>(sinT + (int64_t)pos * P + (l * E) % P, sn);
-#pragma unroll
-      for (int i = 0; i < E; i++) {
-        const float partner = __shfl_xor(g[i], 16, 64);
-        gr[i] = lo ? cs[i] * g[i] + sn[i] * partner : -sn[i] * partner + cs[i] * g[i];
-      }
     } else {
 #pragma unroll
       for (int i = 0; i < E; i += 2) {
         const int p = (l * E + i) / 2;
-        const float c = cosT[(int64_t)pos * P + p], sn = sinT[(int64_t)pos * P + p];
-        gr[i] = c * g[i] + sn * g[i + 1];
-        gr[i + 1] = -sn * g[i] + c * g[i + 1];
+        cs[i] = cs[i + 1] = cosT[(int64_t)pos * P + p];
+        sn[i] = sn[i + 1] = sinT[(int64_t)pos * P + p];
       }
     }
-    if (!qk_norm) {
-      if (live) stE<E>(dst, gr);
-      continue;
-    }
-    float x[E];
-    ldE<E>(qkv + (int64_t)t * nqkv + hh * D + l * E, x);
-    const float* w = (isq ? wq : wk) + l * E;
-    const float ri = rinv[(int64_t)t * (Hq + Hkv) + hh];
-    float dot = 0.f, xn[E];
+    for (int h0 = hw; h0 < H; h0 += 8 * R) {
+      float g[R][E], x[R][E], ri[R];
 #pragma unroll
-    for (int i = 0; i < E; i++) {
-      xn[i] = x[i] * ri;
-      dot += gr[i] * w[i] * xn[i];
-      if (live) {
-        if (isq) aq[i] += gr[i] * xn[i];
-        else ak[i] += gr[i] * xn[i];
+      for (int r = 0; r < R; r++) {
+        const int hh = h0 + 8 * r;
+        if (hh >= H) break;
+        if (hh >= Hq + Hkv) {
+          ld_kv(dv, t, hh - Hq - Hkv, g[r]);
+          continue;
+        }
+        if (hh < Hq) ldE<E>(dq + (int64_t)t * Hq * D + hh * D + l * E, g[r]);
+        else ld_kv(dk, t, hh - Hq, g[r]);
+        if (qk_norm) {
+          ldE<E>(qkv + (int64_t)t * nqkv + hh * D + l * E, x[r]);
+          ri[r] = rinv[(int64_t)t * (Hq + Hkv) + hh];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const int hh = h0 + 8 * r;
+        if (hh >= H) break;
+        TA* dst = dqkv + (int64_t)t * nqkv + hh * D + l * E;
+        if (hh >= Hq + Hkv) {
+          stE<E>(dst, g[r]);
+          continue;
+        }
+        const bool isq = hh < Hq;
+        float gr[E];
+        if (neox) {
+          const bool lo = l * E < P;
+#pragma unroll
+          for (int i = 0; i < E; i++) {
+            const float partner = __shfl_xor(g[r][i], 16, 64);
+            gr[i] = lo ? cs[i] * g[r][i] + sn[i] * partner : -sn[i] * partner + cs[i] * g[r][i];
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < E; i += 2) {
+            gr[i] = cs[i] * g[r][i] + sn[i] * g[r][i + 1];
+            gr[i + 1] = -sn[i] * g[r][i] + cs[i] * g[r][i + 1];
+          }
+        }
+        if (!qk_norm) {
+          stE<E>(dst, gr);
+          continue;
+        }
+        const float* w = (isq ? wq : wk) + l * E;
+        float dot = 0.f, xn[E];
+#pragma unroll
+        for (int i = 0; i < E; i++) {
+          xn[i] = x[r][i] * ri[r];
+          dot += gr[i] * w[i] * xn[i];
+          if (isq) aq[i] += gr[i] * xn[i];
+          else ak[i] += gr[i] * xn[i];
+        }
+        dot = half_sum(dot) / (float)D;
+        float o[E];
+#pragma unroll
+        for (int i = 0; i < E; i++) o[i] = ri[r] * (gr[i] * w[i] - xn[i] * dot);
+        stE<E>(dst, o);
       }
     }
-    dot = half_sum(dot) / (float)D;
-    float o[E];
-#pragma unroll
-    for (int i = 0; i < E; i++) o[i] = ri * (gr[i] * w[i] - xn[i] * dot);
-    if (live) stE<E>(dst, o);
   }
   if (part) {  // block partial of dw: sum the 8 half-waves in a fixed order
     __shared__ float sh[8][2][D];
@@ -389,7 +425,7 @@ int qkv_prep_forward(const void* qkv, int qkv_bf16, void* q, void* k, void* v, f
   SMHIP_REQUIRE(D <= 128 && D % 2 == 0, "qkv prep: head_dim must be even and <= 128");
   const int64_t rows = (int64_t)T * (Hq + 2 * Hkv);
   if (D == 128 || D == 64) {
-    const int gv = gridn(rows, 8);
+    const int gv = (int)std::min<int64_t>(T, (int64_t)num_cus() * 8);  // workgroup per token
 #define SMHIP_QKV_FWD(DD, TT, TQ) \
   hipLaunchKernelGGL((qkv_prep_fwd_vec_kernel<DD, TT, TQ>), dim3(gv), dim3(256), 0, s, (const TQ*)qkv, (TT*)q, (TT*)k, (TT*)v, rinv, wq, wk, cosT, sinT, T, S, Hq, Hkv, qk_norm, neox, eps)
     if (qkv_bf16) {
@@ -424,8 +460,9 @@ int qkv_prep_backward(const void* dq_, const void* dk_, const void* dv_, int gra
   const int64_t rows = (int64_t)T * (Hq + 2 * Hkv);
   const bool want_dw = qk_norm && (dwq || dwk);
   const bool vec = D == 128 || D == 64;
-  // dw partials: one row of 2*D per block, so fewer (larger) blocks when they are needed
-  const int g = vec ? gridn(rows, 8, want_dw ? 2 : 8) : gridn(rows, 4, 2);
+  // dw partials: one row of 2*D per block, so fewer (larger) blocks when they are needed; the
+  // vectorised kernel runs a workgroup per token
+  const int g = vec ? (int)std::min<int64_t>(T, (int64_t)num_cus() * (want_dw ? 2 : 8)) : gridn(rows, 4, 2);
   float* part = nullptr;
   if (want_dw) {
     part = (float*)workspace(s, sizeof(float) * (size_t)g * 2 * D, 7);
