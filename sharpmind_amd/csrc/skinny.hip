@@ -332,7 +332,18 @@ __global__ __launch_bounds__(256) void skinny_reduce_batch_kernel(BatchArgs b) {
   typedef float f4v __attribute__((ext_vector_type(4)));
   const f4v* p4 = reinterpret_cast<const f4v*>(j.partial) + q;
   f4v acc = {0.f, 0.f, 0.f, 0.f};
-  for (int sidx = 0; sidx < j.S; sidx++) acc += __builtin_nontemporal_load(p4 + sidx * plane);
+  int sidx = 0;
+  for (; sidx + 4 <= j.S; sidx += 4) {  // four loads in flight, added in split order
+    const f4v a0 = __builtin_nontemporal_load(p4 + (sidx + 0) * plane);
+    const f4v a1 = __builtin_nontemporal_load(p4 + (sidx + 1) * plane);
+    const f4v a2 = __builtin_nontemporal_load(p4 + (sidx + 2) * plane);
+    const f4v a3 = __builtin_nontemporal_load(p4 + (sidx + 3) * plane);
+    acc += a0;
+    acc += a1;
+    acc += a2;
+    acc += a3;
+  }
+  for (; sidx < j.S; sidx++) acc += __builtin_nontemporal_load(p4 + sidx * plane);
   const float v[4] = {acc[0], acc[1], acc[2], acc[3]};
 #pragma unroll
   for (int e = 0; e < 4; e++) {
