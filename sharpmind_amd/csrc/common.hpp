@@ -169,6 +169,8 @@ struct GemmArgs {
   const int* mask_cols;
   int mask_rank, mask_nblk;
   int* masked;
+  // rank-sized products: hold the launch so the next product with this hold shares it
+  struct SkinnyHold* hold;
 };
 int gemm(const GemmArgs& g, hipStream_t s);
 

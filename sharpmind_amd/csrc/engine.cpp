@@ -85,6 +85,7 @@ struct Engine {
   bool base_ws = false;
   uint16_t *emb_b = nullptr, *emb_bt = nullptr;
   SkinnyBatch skb;                // deferred split reductions of a layer's adapter gradients
+  SkinnyHold skh;                 // a projection's dB product waiting to share its launch with dA
   int lb_masked[4] = {};          // the last dB product of projection p applied the block-diagonal mask
   DequantJob* dq_jobs = nullptr;  // device table of the per-step decode (one launch)
   int dq_njobs = 0;
@@ -482,6 +483,7 @@ static int proj_backward(Engine* e, int l, int p, const void* dY, const float* d
     gb.C = w.lb[p].grad; gb.ldc = Out;
     gb.split_k = split_arg(e, nr, Out, T);
     gb.defer = &e->skb;
+    gb.hold = &e->skh;
     if (e->nblk[p] > 1) {  // fused q|k|v or gate|up: only the diagonal blocks of dB are gradients
       gb.mask_cols = p == P_QKV ? w.lb_cols : w.lb_cols + 3;
       gb.mask_rank = e->c.lora_rank;
@@ -498,7 +500,9 @@ static int proj_backward(Engine* e, int l, int p, const void* dY, const float* d
     ga.C = w.la[p].grad; ga.ldc = nr;
     ga.split_k = split_arg(e, In, nr, T);
     ga.defer = &e->skb;
+    ga.hold = &e->skh;
     if (int rc = gemm(ga, s)) return rc;
+    if (int rc = skinny_release(&e->skh, s)) return rc;  // when the two did not pair
     g.K2 = nr;
     g.A2 = act_k(e, e->z, nr);
     g.B2 = lora_op(e, w.la[p], true, nr);

@@ -838,10 +838,10 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   if (g.K2 == 0 && !g.bias && !g.R && (g.N <= 64 || g.M <= 64) && (bm == SRC_BF16_K || bm == SRC_BF16_R)) {
     const int r = g.N <= 64
         ? gemm_skinny(g.M, g.N, g.K, g.A.p, g.A.ld, am == SRC_BF16_K, g.B.p, g.B.ld, bm == SRC_BF16_K, g.alpha,
-                      g.beta, g.C, g.ldc, false, g.c_bf16 != 0, g.defer, s)
+                      g.beta, g.C, g.ldc, false, g.c_bf16 != 0, g.defer, s, SkinnyMask{}, g.hold)
         : gemm_skinny(g.N, g.M, g.K, g.B.p, g.B.ld, bm == SRC_BF16_K, g.A.p, g.A.ld, am == SRC_BF16_K, g.alpha,
                       g.beta, g.C, g.ldc, true, g.c_bf16 != 0, g.defer, s,
-                      SkinnyMask{g.mask_cols, g.mask_rank, g.mask_nblk});
+                      SkinnyMask{g.mask_cols, g.mask_rank, g.mask_nblk}, g.hold);
     if (r > 0 && g.M <= 64 && g.N > 64 && g.mask_cols && g.masked) *g.masked = 1;
     if (r != 0) return r;
   }

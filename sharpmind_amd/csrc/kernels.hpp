@@ -67,9 +67,18 @@ struct SkinnyBatch {
   SkinnyJob job[kMaxJobs];
 };
 int skinny_flush(SkinnyBatch* b, hipStream_t s);
+// A rank-sized product whose launch is held back so the next compatible one (same operand kinds,
+// rank and output type) shares its launch.  skinny_release launches whatever is still held.
+struct SkinnyHold {
+  bool valid = false;
+  bool big_k, small_k, trans, c_bf16;
+  int mt, S, n, M, K;
+  unsigned char args[256];  // the product's kernel arguments (sk::Args)
+};
+int skinny_release(SkinnyHold* h, hipStream_t s);
 int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, const void* small, int64_t lds,
                 bool small_k, float alpha, float beta, void* C, int64_t ldc, bool trans_out, bool c_bf16,
-                SkinnyBatch* defer, hipStream_t s, SkinnyMask mask = SkinnyMask{});
+                SkinnyBatch* defer, hipStream_t s, SkinnyMask mask = SkinnyMask{}, SkinnyHold* hold = nullptr);
 
 // quant.hip
 int dequant_raw(int qtype, const void* raw, float* out, int64_t n, hipStream_t s);

@@ -21,6 +21,8 @@
 // The reduction over K is split S ways (S chosen so the fp32 partials stay a small fraction
 // of the bytes of Big); a second kernel sums the S partials in a fixed order, so results are
 // deterministic and independent of timing.
+#include <cstring>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -175,13 +177,12 @@ struct SmallLoad {
   }
 };
 
+// one 128-row tile and one K split of a product (the kernels below pick which)
 template <bool BIGK, bool SMALLK, int NB, bool TRANS_OUT, bool C_BF16>
-__global__ __launch_bounds__(256, 2) void skinny_kernel(Args a) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[ST * STAGE];
+__device__ __forceinline__ void skinny_tile(const Args& a, int mtile, int split, uint8_t* smem) {
   auto big_st = [&](int s) -> uint8_t* { return smem + s * STAGE; };
   auto small_st = [&](int s) -> uint8_t* { return smem + s * STAGE + BIG_BYTES; };
-  const int m0 = blockIdx.x * MT;
-  const int split = blockIdx.y;
+  const int m0 = mtile * MT;
   const int kt0 = split * a.kps;
   const int nk = max(0, min(a.K / BKT, kt0 + a.kps) - kt0);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -258,6 +259,22 @@ __global__ __launch_bounds__(256, 2) void skinny_kernel(Args a) {
         }
       }
     }
+}
+
+template <bool BIGK, bool SMALLK, int NB, bool TRANS_OUT, bool C_BF16>
+__global__ __launch_bounds__(256, 2) void skinny_kernel(Args a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[ST * STAGE];
+  skinny_tile<BIGK, SMALLK, NB, TRANS_OUT, C_BF16>(a, blockIdx.x, blockIdx.y, smem);
+}
+
+// Two products of the same operand kinds and rank in one launch (a LoRA projection's dA and
+// dB^T): workgroups [0, nb0) are the (tile, split) pairs of a0, the rest those of a1.
+template <bool BIGK, bool SMALLK, int NB, bool T0, bool T1, bool C_BF16>
+__global__ __launch_bounds__(256, 2) void skinny_pair_kernel(Args a0, Args a1, int mt0, int nb0, int mt1) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[ST * STAGE];
+  const int b = blockIdx.x;
+  if (b < nb0) skinny_tile<BIGK, SMALLK, NB, T0, C_BF16>(a0, b % mt0, b / mt0, smem);
+  else skinny_tile<BIGK, SMALLK, NB, T1, C_BF16>(a1, (b - nb0) % mt1, (b - nb0) / mt1, smem);
 }
 
 // C (m, r) = alpha * sum_s partial[s][m][r] + beta * C, splits summed in ascending order.
@@ -404,10 +421,28 @@ int skinny_flush(SkinnyBatch* b, hipStream_t s) {
   return SMHIP_OK;
 }
 
+int skinny_release(SkinnyHold* h, hipStream_t s) {
+  using namespace sk;
+  if (!h || !h->valid) return SMHIP_OK;
+  h->valid = false;
+  Args a;
+  memcpy(&a, h->args, sizeof(Args));
+  const int ev0 = prof_mark(s);
+  const dim3 grid(h->mt, h->S);
+  if (h->big_k && h->small_k) launch_nb<true, true>(h->n / 16, a, grid, h->trans, h->c_bf16, s);
+  else if (h->big_k) launch_nb<true, false>(h->n / 16, a, grid, h->trans, h->c_bf16, s);
+  else if (h->small_k) launch_nb<false, true>(h->n / 16, a, grid, h->trans, h->c_bf16, s);
+  else launch_nb<false, false>(h->n / 16, a, grid, h->trans, h->c_bf16, s);
+  SMHIP_CHECK_LAUNCH();
+  prof_add(PROF_GEMM, ev0, prof_mark(s), 2.0 * h->M * h->n * (double)h->K, h->M, h->n, h->K);
+  return SMHIP_OK;
+}
+
 int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, const void* small, int64_t lds,
                 bool small_k, float alpha, float beta, void* C, int64_t ldc, bool trans_out, bool c_bf16,
-                SkinnyBatch* defer, hipStream_t s, SkinnyMask mask) {
+                SkinnyBatch* defer, hipStream_t s, SkinnyMask mask, SkinnyHold* hold) {
   using namespace sk;
+  static_assert(sizeof(Args) <= sizeof(SkinnyHold::args), "SkinnyHold::args holds an sk::Args");
   if (n < 1 || n > 64 || n % 16 || M < 1 || K < BKT || K % BKT) return 0;
   if (((uintptr_t)big | (uintptr_t)small) % 16 || ldb % 8) return 0;
   if (small_k && lds % 8) return 0;
@@ -436,8 +471,10 @@ int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, c
   const size_t pbytes = (sizeof(float) * (size_t)S * M * n + 255) & ~(size_t)255;
   const bool deferred = S > 1 && defer && pbytes <= defer->cap;
   if (deferred) {
-    if (defer->n == SkinnyBatch::kMaxJobs || defer->used + pbytes > defer->cap)
+    if (defer->n == SkinnyBatch::kMaxJobs || defer->used + pbytes > defer->cap) {
+      if (int rc = skinny_release(hold, s)) return rc;  // its partials are in the batch being reduced
       if (int rc = skinny_flush(defer, s)) return rc;
+    }
     a.partial = (float*)((char*)defer->arena + defer->used);
     defer->job[defer->n++] = SkinnyJob{a.partial, C, ldc, S, M, n, alpha, beta, trans_out ? 1 : 0, c_bf16 ? 1 : 0, mask};
     defer->used += pbytes;
@@ -446,6 +483,42 @@ int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, c
     if (!a.partial) return fail(SMHIP_ENOMEM, "gemm_skinny: split workspace");
   }
   const dim3 grid(mt, S);
+  // a held launch: products whose partials need no reduction launch of their own can share one
+  if (hold && !(S > 1 && !deferred)) {
+    if (hold->valid && hold->big_k == big_k && hold->small_k == small_k && hold->n == n &&
+        hold->c_bf16 == c_bf16 && !big_k && !small_k) {
+      Args a0;
+      memcpy(&a0, hold->args, sizeof(Args));
+      const int nb0 = hold->mt * hold->S;
+      const dim3 g2(nb0 + mt * S);
+      const int ev0 = prof_mark(s);
+#define SMHIP_PAIR(NBV, T0, T1)                                                                                \
+  if (c_bf16) hipLaunchKernelGGL((skinny_pair_kernel<false, false, NBV, T0, T1, true>), g2, dim3(256), 0, s, a0, a, hold->mt, nb0, mt); \
+  else hipLaunchKernelGGL((skinny_pair_kernel<false, false, NBV, T0, T1, false>), g2, dim3(256), 0, s, a0, a, hold->mt, nb0, mt);
+#define SMHIP_PAIR_T(NBV)                                                                                      \
+  if (hold->trans) { if (trans_out) { SMHIP_PAIR(NBV, true, true) } else { SMHIP_PAIR(NBV, true, false) } }      \
+  else { if (trans_out) { SMHIP_PAIR(NBV, false, true) } else { SMHIP_PAIR(NBV, false, false) } }
+      switch (n / 16) {
+        case 1: SMHIP_PAIR_T(1) break;
+        case 2: SMHIP_PAIR_T(2) break;
+        case 3: SMHIP_PAIR_T(3) break;
+        default: SMHIP_PAIR_T(4) break;
+      }
+#undef SMHIP_PAIR_T
+#undef SMHIP_PAIR
+      SMHIP_CHECK_LAUNCH();
+      prof_add(PROF_GEMM, ev0, prof_mark(s), 2.0 * ((double)hold->M * hold->n * hold->K + (double)M * n * K), M, n, K);
+      hold->valid = false;
+      return 1;
+    }
+    if (hold->valid)
+      if (int rc = skinny_release(hold, s)) return rc;
+    hold->valid = true;
+    hold->big_k = big_k; hold->small_k = small_k; hold->trans = trans_out; hold->c_bf16 = c_bf16;
+    hold->mt = mt; hold->S = S; hold->n = n; hold->M = M; hold->K = K;
+    memcpy(hold->args, &a, sizeof(Args));
+    return 1;
+  }
   const int ev0 = prof_mark(s);
   if (big_k && small_k) launch_nb<true, true>(n / 16, a, grid, trans_out, c_bf16, s);
   else if (big_k) launch_nb<true, false>(n / 16, a, grid, trans_out, c_bf16, s);
