@@ -196,10 +196,13 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_fwd_kernel(const uint16_t
     rs += __shfl_xor(rs, 32, 64);
     l = l * alpha + rs;
     m = mnew;
+    // rescale only when some query's running max moved (alpha == 1 multiplies are exact no-ops)
+    if (__any(alpha != 1.f)) {
 #pragma unroll
-    for (int i = 0; i < D / 32; i++)
+      for (int i = 0; i < D / 32; i++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) oacc[i][e] *= alpha;
+        for (int e = 0; e < 16; e++) oacc[i][e] *= alpha;
+    }
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       const bf16x8 pf = pack8(sacc[c >> 1], 8 * (c & 1));
