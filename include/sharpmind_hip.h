@@ -14,7 +14,10 @@
  *    reference's GradientMapping contract (SharpMind.Core/Training/
  *    GradientMapping.cs:7-16).
  *  - Thread safety: entries are re-entrant.  Internal scratch is keyed by stream;
- *    calls issued concurrently from several threads must use distinct streams.
+ *    device entries issued concurrently from several threads must use distinct streams.
+ *    smhip_host_* entries run on a stream (and scratch) private to the calling thread, so
+ *    they may be called concurrently, as the reference's Parallel.For bodies call its slots
+ *    (BackpropEngine.cs:563-582).
  */
 #ifndef SHARPMIND_HIP_H
 #define SHARPMIND_HIP_H
@@ -207,9 +210,23 @@ int smhip_engine_get_tensor(void* engine, const char* name, int which, void* hos
 /* Synthetic initialisation on the device: N(0,0.02) weights (quantised in LoRA mode), norms 1,
  * biases 0, LoRA A Kaiming-uniform, B ~ N(0,1e-3). */
 int smhip_engine_init_synthetic(void* engine, uint64_t seed);
-/* ids/labels: device int32 [batch*seq] (label -100 = ignored); loss: device float or NULL. */
+/* ids/labels: device int32 [batch*seq] (label -100 = ignored); loss: device float or NULL.
+ * Zeroes the gradients first (optimizer.ZeroGrad at the start of a window, TrainLoop.cs:108-109),
+ * then runs TrainLoop.ForwardBackward (TrainLoop.cs:222-243). */
 int smhip_engine_forward_backward(void* engine, const int32_t* ids, const int32_t* labels, float* loss,
                                   smhip_stream_t stream);
+/* Gradient accumulation over micro-batches (TrainLoop.RunAsync, TrainLoop.cs:104-120): with
+ * accumulate != 0 the gradients of this micro-batch are ADDED to those already held (no zeroing),
+ * so GradAccumSteps micro-batches followed by one optimizer step reproduce the reference loop.
+ * accumulate == 0 is smhip_engine_forward_backward. */
+int smhip_engine_forward_backward_accum(void* engine, const int32_t* ids, const int32_t* labels, float* loss,
+                                        int accumulate, smhip_stream_t stream);
+/* optimizer.ZeroGrad (Optimizers/AdamW.cs:91-94): all trainable gradients to 0 on `stream`. */
+int smhip_engine_zero_grad(void* engine, smhip_stream_t stream);
+/* _optimizer.LearningRate = _scheduler.GetLr(step + 1) (TrainLoop.cs:122-123): the learning rate the
+ * next smhip_engine_optimizer_step uses.  Finite and >= 0. */
+int smhip_engine_set_lr(void* engine, float lr);
+int smhip_engine_get_lr(void* engine, float* lr);
 /* Clip (if configured) + AdamW; grad_norm_sq: device float or NULL (pre-clip sum of squares). */
 int smhip_engine_optimizer_step(void* engine, float* grad_norm_sq, smhip_stream_t stream);
 int smhip_engine_step(void* engine, const int32_t* ids, const int32_t* labels, float* loss,

@@ -29,8 +29,18 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
 
-def _compile(src):
+def _headers():
+    inc = os.path.join(HERE, "..", "include")
+    hs = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hpp", ".h"))]
+    return hs + [os.path.join(inc, f) for f in os.listdir(inc)]
+
+
+def _compile(src, incremental=False):
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    if incremental and os.path.exists(obj):
+        newest = max(os.path.getmtime(p) for p in [src] + _headers())
+        if os.path.getmtime(obj) >= newest:
+            return obj
     cmd = [HIPCC] + CFLAGS + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -38,12 +48,16 @@ def _compile(src):
     return obj
 
 
-def build(verbose=True):
+def build(verbose=True, incremental=None):
+    """Compile every source (incremental=True, or SMHIP_INCREMENTAL=1: only sources newer than
+    their object or with a newer header) and link the library."""
+    if incremental is None:
+        incremental = os.environ.get("SMHIP_INCREMENTAL") == "1"
     os.makedirs(BUILD, exist_ok=True)
     srcs = sources()
     jobs = min(len(srcs), int(os.environ.get("MAX_JOBS", "8")), 16)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, srcs))
+        objs = list(ex.map(lambda f: _compile(f, incremental), srcs))
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", OUT] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:

@@ -66,6 +66,18 @@ void* workspace(hipStream_t s, size_t bytes, int slot) {
   return b.p;
 }
 
+void workspace_release(hipStream_t s) {
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  for (auto it = g_ws.begin(); it != g_ws.end();) {
+    if (it->first.s == s) {
+      if (it->second.p) hipFree(it->second.p);
+      it = g_ws.erase(it);
+    } else {
+      ++it;
+    }
+  }
+}
+
 struct Profiler {
   std::vector<hipEvent_t> ev;
   size_t used = 0;
@@ -380,38 +392,85 @@ int smhip_attention_forward_probs(const float* q, const float* k, const float* v
 }  // extern "C"
 
 // ---------------------------------------------------------------- host-pointer slot entries
+// The reference calls its slots concurrently from Parallel.For bodies (_mapping.Attention per
+// batch row, BackpropEngine.cs:563-582), so every host entry runs on a stream owned by the
+// calling thread (one per device).  Internal scratch is keyed by stream, so two threads never
+// share a split-K partial or a dP buffer, and a thread's grow-only device buffers are reused
+// from call to call instead of being allocated and freed each time.
 namespace {
 
+struct HostCtx {
+  hipStream_t s = nullptr;
+  std::vector<std::pair<void*, size_t>> bufs;  // argument slot -> device buffer
+  ~HostCtx() {
+    if (s) {
+      hipStreamSynchronize(s);
+      workspace_release(s);
+      hipStreamDestroy(s);
+    }
+    for (auto& b : bufs)
+      if (b.first) hipFree(b.first);
+  }
+};
+thread_local std::unordered_map<int, HostCtx> t_host;
+
 struct DevArena {
-  std::vector<void*> ptrs;
+  HostCtx* ctx = nullptr;
+  hipStream_t s = nullptr;
   int rc = SMHIP_OK;
-  ~DevArena() {
-    for (void* p : ptrs) hipFree(p);
+  int next = 0;  // argument slot of the next buffer
+  DevArena() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) { rc = fail(SMHIP_EHIP, "host entry: no HIP device"); return; }
+    ctx = &t_host[dev];
+    // default priority, non-blocking: the calling thread's private queue
+    if (!ctx->s && hipStreamCreateWithFlags(&ctx->s, hipStreamNonBlocking) != hipSuccess) {
+      ctx->s = nullptr;
+      rc = fail(SMHIP_EHIP, "host entry: hipStreamCreate failed");
+      return;
+    }
+    s = ctx->s;
+  }
+  void* slot(size_t bytes) {
+    if (rc) return nullptr;
+    const int k = next++;
+    if ((int)ctx->bufs.size() <= k) ctx->bufs.resize(k + 1, {nullptr, 0});
+    auto& b = ctx->bufs[k];
+    if (b.second < bytes || !b.first) {
+      if (b.first) {
+        hipStreamSynchronize(s);  // an earlier call that failed part-way may still be queued
+        hipFree(b.first);
+        b = {nullptr, 0};
+      }
+      size_t want = ((bytes < 256 ? 256 : bytes) + 4095) & ~(size_t)4095;
+      if (hipMalloc(&b.first, want) != hipSuccess) { b = {nullptr, 0}; rc = fail(SMHIP_ENOMEM, "host entry: hipMalloc failed"); return nullptr; }
+      b.second = want;
+    }
+    return b.first;
   }
   template <typename T>
-  T* up(const T* h, size_t n) {  // allocate + copy host -> device (n elements)
-    if (rc) return nullptr;
-    void* d = nullptr;
-    size_t bytes = n * sizeof(T);
-    if (hipMalloc(&d, bytes ? bytes : 16) != hipSuccess) { rc = fail(SMHIP_ENOMEM, "host entry: hipMalloc failed"); return nullptr; }
-    ptrs.push_back(d);
-    if (h && bytes && hipMemcpy(d, h, bytes, hipMemcpyHostToDevice) != hipSuccess) { rc = fail(SMHIP_EHIP, "host entry: H2D copy failed"); return nullptr; }
+  T* up(const T* h, size_t n) {  // device copy of n host elements
+    const size_t bytes = n * sizeof(T);
+    void* d = slot(bytes);
+    if (!d) return nullptr;
+    if (h && bytes && hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, s) != hipSuccess) { rc = fail(SMHIP_EHIP, "host entry: H2D copy failed"); return nullptr; }
     return (T*)d;
   }
   template <typename T>
   T* zeros(size_t n) {
     T* d = up<T>(nullptr, n);
-    if (d && n && hipMemset(d, 0, n * sizeof(T)) != hipSuccess) rc = fail(SMHIP_EHIP, "host entry: memset failed");
+    if (d && n && hipMemsetAsync(d, 0, n * sizeof(T), s) != hipSuccess) rc = fail(SMHIP_EHIP, "host entry: memset failed");
     return d;
   }
   template <typename T>
   void down(T* h, const T* d, size_t n) {
     if (rc || !h || !n) return;
-    if (hipMemcpy(h, d, n * sizeof(T), hipMemcpyDeviceToHost) != hipSuccess) rc = fail(SMHIP_EHIP, "host entry: D2H copy failed");
+    if (hipMemcpyAsync(h, d, n * sizeof(T), hipMemcpyDeviceToHost, s) != hipSuccess) { rc = fail(SMHIP_EHIP, "host entry: D2H copy failed"); return; }
+    if (hipStreamSynchronize(s) != hipSuccess) rc = fail(SMHIP_EHIP, "host entry: synchronize failed");
   }
   int sync() {
     if (rc) return rc;
-    hipError_t e = hipDeviceSynchronize();
+    hipError_t e = hipStreamSynchronize(s);
     if (e != hipSuccess) rc = fail(SMHIP_EHIP, std::string("host entry: ") + hipGetErrorString(e));
     return rc;
   }
@@ -431,7 +490,7 @@ int smhip_host_grad_linear(const float* dY, const float* X, const float* W, floa
   float* ddb = db ? a.up(db, (size_t)Out) : nullptr;
   float* ddX = dX ? a.zeros<float>((size_t)M * In) : nullptr;
   if (a.rc) return a.rc;
-  int rc = smhip_grad_linear(ddY, dXin, dWt, ddW, ddb, ddX, M, In, Out, precision, nullptr);
+  int rc = smhip_grad_linear(ddY, dXin, dWt, ddW, ddb, ddX, M, In, Out, precision, a.s);
   if (rc) return rc;
   if (a.sync()) return a.rc;
   a.down(dX, ddX, (size_t)M * In);
@@ -446,7 +505,7 @@ int smhip_host_grad_rmsnorm(const float* dY, const float* xNorm, const float* rm
   float *p1 = a.up(dY, (size_t)T * D), *p2 = a.up(xNorm, (size_t)T * D), *p3 = a.up(rmsInv, (size_t)T);
   float *p4 = a.up(w, (size_t)D), *p5 = dw ? a.up(dw, (size_t)D) : nullptr, *p6 = a.zeros<float>((size_t)T * D);
   if (a.rc) return a.rc;
-  int rc = smhip_grad_rmsnorm(p1, p2, p3, p4, p5, p6, T, D, nullptr);
+  int rc = smhip_grad_rmsnorm(p1, p2, p3, p4, p5, p6, T, D, a.s);
   if (rc) return rc;
   if (a.sync()) return a.rc;
   a.down(dX, p6, (size_t)T * D);
@@ -461,7 +520,7 @@ int smhip_host_grad_layernorm(const float* dY, const float* x, const float* w, f
   float *p4 = dw ? a.up(dw, (size_t)D) : nullptr, *p5 = db ? a.up(db, (size_t)D) : nullptr;
   float* p6 = a.zeros<float>((size_t)T * D);
   if (a.rc) return a.rc;
-  int rc = smhip_grad_layernorm(p1, p2, p3, p4, p5, p6, T, D, eps, nullptr);
+  int rc = smhip_grad_layernorm(p1, p2, p3, p4, p5, p6, T, D, eps, a.s);
   if (rc) return rc;
   if (a.sync()) return a.rc;
   a.down(dX, p6, (size_t)T * D);
@@ -478,7 +537,7 @@ int smhip_host_grad_attention(const float* dO, const float* q, const float* k, c
   float *p1 = a.up(dO, sd), *p2 = a.up(q, sd), *p3 = a.up(k, sd), *p4 = a.up(v, sd), *p5 = a.up(probs, (size_t)S * S);
   float *o1 = a.zeros<float>(sd), *o2 = a.zeros<float>(sd), *o3 = a.zeros<float>(sd);
   if (a.rc) return a.rc;
-  int rc = smhip_grad_attention(p1, p2, p3, p4, p5, o1, o2, o3, S, D, scale, nullptr);
+  int rc = smhip_grad_attention(p1, p2, p3, p4, p5, o1, o2, o3, S, D, scale, a.s);
   if (rc) return rc;
   if (a.sync()) return a.rc;
   a.down(dQ, o1, sd);
@@ -493,7 +552,7 @@ int smhip_host_grad_embedding(const float* dY, const int32_t* ids, float* dE, in
   int32_t* p2 = a.up(ids, (size_t)T);
   float* p3 = a.up(dE, (size_t)V * D);
   if (a.rc) return a.rc;
-  int rc = smhip_grad_embedding(p1, p2, p3, T, D, V, nullptr);
+  int rc = smhip_grad_embedding(p1, p2, p3, T, D, V, a.s);
   if (rc) return rc;
   if (a.sync()) return a.rc;
   a.down(dE, p3, (size_t)V * D);
@@ -504,7 +563,7 @@ int smhip_host_grad_silu(const float* dY, const float* x, float* dX, int64_t n) 
   DevArena a;
   float *p1 = a.up(dY, (size_t)n), *p2 = a.up(x, (size_t)n), *p3 = a.zeros<float>((size_t)n);
   if (a.rc) return a.rc;
-  int rc = smhip_grad_silu(p1, p2, p3, n, nullptr);
+  int rc = smhip_grad_silu(p1, p2, p3, n, a.s);
   if (rc) return rc;
   if (a.sync()) return a.rc;
   a.down(dX, p3, (size_t)n);
@@ -515,7 +574,7 @@ int smhip_host_grad_gelu(const float* dY, const float* x, float* dX, int64_t n) 
   DevArena a;
   float *p1 = a.up(dY, (size_t)n), *p2 = a.up(x, (size_t)n), *p3 = a.zeros<float>((size_t)n);
   if (a.rc) return a.rc;
-  int rc = smhip_grad_gelu(p1, p2, p3, n, nullptr);
+  int rc = smhip_grad_gelu(p1, p2, p3, n, a.s);
   if (rc) return rc;
   if (a.sync()) return a.rc;
   a.down(dX, p3, (size_t)n);
@@ -528,7 +587,7 @@ int smhip_host_adamw_update(float* data, const float* grad, float* m, float* v, 
   DevArena a;
   float *p1 = a.up(data, (size_t)n), *p2 = a.up(grad, (size_t)n), *p3 = a.up(m, (size_t)n), *p4 = a.up(v, (size_t)n);
   if (a.rc) return a.rc;
-  int rc = smhip_adamw_update(p1, p2, p3, p4, n, beta1, beta2, bc1, bc2, lr, eps, decay, nullptr);
+  int rc = smhip_adamw_update(p1, p2, p3, p4, n, beta1, beta2, bc1, bc2, lr, eps, decay, a.s);
   if (rc) return rc;
   if (a.sync()) return a.rc;
   a.down(data, p1, (size_t)n);
@@ -542,7 +601,7 @@ int smhip_host_l2normsq(const float* data, int64_t n, float* out) {
   float* p1 = a.up(data, (size_t)n);
   float* p2 = a.zeros<float>(1);
   if (a.rc) return a.rc;
-  int rc = smhip_l2normsq(p1, n, p2, nullptr);
+  int rc = smhip_l2normsq(p1, n, p2, a.s);
   if (rc) return rc;
   if (a.sync()) return a.rc;
   a.down(out, p2, 1);
@@ -560,7 +619,7 @@ int smhip_host_qmatmul(int qtype, const float* in, const void* rawW, float* out,
   uint8_t* p2 = a.up((const uint8_t*)rawW, wbytes);
   float* p3 = a.zeros<float>((size_t)M * N);
   if (a.rc) return a.rc;
-  int rc = smhip_qmatmul(qtype, p1, p2, p3, M, K, N, SMHIP_PREC_FP32, nullptr);
+  int rc = smhip_qmatmul(qtype, p1, p2, p3, M, K, N, SMHIP_PREC_FP32, a.s);
   if (rc) return rc;
   if (a.sync()) return a.rc;
   a.down(out, p3, (size_t)M * N);

@@ -32,6 +32,8 @@ int fail(int code, const std::string& msg);
 // buffer keyed by stream is never used by two kernels at once; calls from
 // different threads must use different streams (documented in the header).
 void* workspace(hipStream_t s, size_t bytes, int slot = 0);
+// Frees every buffer keyed by stream s (the stream's work must be complete).
+void workspace_release(hipStream_t s);
 
 // ---------------------------------------------------------------- bf16
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

@@ -537,7 +537,8 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
   const int T = e->T, d = c.d_model, F = c.ffn_dim, V = c.vocab, Hq = c.n_heads, Hkv = c.n_kv_heads, D = c.head_dim;
   int rc;
 #define R_(x) do { if ((rc = (x))) return rc; } while (0)
-  R_(zero_bytes(e->grad, sizeof(float) * (size_t)e->n_train, s));  // optimizer.ZeroGrad (TrainLoop.cs:109)
+  // gradients accumulate (+=) into the arena; the caller zeroes it at the start of an
+  // accumulation window (optimizer.ZeroGrad, TrainLoop.cs:108-109)
 
   // decode the frozen base into the bf16 workspace (both layouts), all matrices in one launch
   if (e->base_ws) R_(dequant_bf16_many(e->dq_jobs, e->dq_njobs, e->dq_tiles, s));
@@ -1305,11 +1306,36 @@ static int forward_backward_graph(Engine* e, const int32_t* ids, const int32_t* 
   return SMHIP_OK;
 }
 
+int smhip_engine_zero_grad(void* engine, smhip_stream_t stream) {
+  SMHIP_REQUIRE(engine, "engine: null handle");
+  Engine* e = (Engine*)engine;
+  return zero_bytes(e->grad, sizeof(float) * (size_t)e->n_train, (hipStream_t)stream);
+}
+
+int smhip_engine_set_lr(void* engine, float lr) {
+  SMHIP_REQUIRE(engine, "engine: null handle");
+  SMHIP_REQUIRE(std::isfinite(lr) && lr >= 0.f, "engine_set_lr: learning rate must be finite and >= 0");
+  ((Engine*)engine)->c.lr = lr;
+  return SMHIP_OK;
+}
+
+int smhip_engine_get_lr(void* engine, float* lr) {
+  SMHIP_REQUIRE(engine && lr, "engine_get_lr: null argument");
+  *lr = ((Engine*)engine)->c.lr;
+  return SMHIP_OK;
+}
+
 int smhip_engine_forward_backward(void* engine, const int32_t* ids, const int32_t* labels, float* loss,
                                   smhip_stream_t stream) {
+  return smhip_engine_forward_backward_accum(engine, ids, labels, loss, 0, stream);
+}
+
+int smhip_engine_forward_backward_accum(void* engine, const int32_t* ids, const int32_t* labels, float* loss,
+                                        int accumulate, smhip_stream_t stream) {
   SMHIP_REQUIRE(engine && ids && labels, "engine_forward_backward: null argument");
   Engine* e = (Engine*)engine;
   int rc;
+  if (!accumulate && (rc = smhip_engine_zero_grad(engine, stream))) return rc;
   if (e->use_graph && !profiling_active()) rc = forward_backward_graph(e, ids, labels, (hipStream_t)stream);
   else rc = forward_backward(e, ids, labels, (hipStream_t)stream);
   if (rc) return rc;

@@ -90,9 +90,26 @@ class Engine:
     def _stream():
         return torch.cuda.current_stream().cuda_stream
 
-    def forward_backward(self, ids, labels, loss=None):
-        check(lib().smhip_engine_forward_backward(self.h, ids.data_ptr(), labels.data_ptr(),
-                                                  loss.data_ptr() if loss is not None else None, self._stream()))
+    def forward_backward(self, ids, labels, loss=None, accumulate=False):
+        """TrainLoop.ForwardBackward; accumulate=True adds to the held gradients (a later micro-batch of a
+        GradAccumSteps window, TrainLoop.cs:104-120), otherwise they are zeroed first."""
+        check(lib().smhip_engine_forward_backward_accum(self.h, ids.data_ptr(), labels.data_ptr(),
+                                                        loss.data_ptr() if loss is not None else None,
+                                                        1 if accumulate else 0, self._stream()))
+
+    def zero_grad(self):
+        check(lib().smhip_engine_zero_grad(self.h, self._stream()))
+
+    @property
+    def lr(self):
+        v = ctypes.c_float()
+        check(lib().smhip_engine_get_lr(self.h, ctypes.byref(v)))
+        return v.value
+
+    @lr.setter
+    def lr(self, value):
+        """_optimizer.LearningRate = scheduler.GetLr(step + 1) (TrainLoop.cs:122-123)."""
+        check(lib().smhip_engine_set_lr(self.h, float(value)))
 
     def optimizer_step(self, grad_norm_sq=None):
         check(lib().smhip_engine_optimizer_step(self.h, grad_norm_sq.data_ptr() if grad_norm_sq is not None else None,

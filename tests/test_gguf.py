@@ -67,3 +67,33 @@ def test_not_gguf_is_an_error(tmp_path):
     trunc.write_bytes(path.read_bytes()[:200])
     with pytest.raises(SmHipError):
         gguf_tensor_table(trunc)
+
+
+def test_hand_assembled_header(tmp_path):
+    """A file laid out byte by byte from the published GGUF v3 layout (magic "GGUF", u32 version,
+    u64 tensor and KV counts, u64-length strings, u32 value types, tensor infos of name / u32 n_dims /
+    u64 dims innermost first / u32 ggml type / u64 offset from the data section, the data section
+    aligned to general.alignment), written without oracle/gguf.py's writer.  Offsets by hand:
+    header = 24 + 45 (architecture) + 33 (alignment) + 57 + 50 (tensor infos) = 209 bytes, data at
+    256; token_embd (Q8_0, 4 rows x 64) takes 4*2*34 = 272 bytes, so output_norm sits at 320."""
+    import struct
+
+    def s(x):
+        return struct.pack("<Q", len(x)) + x.encode()
+
+    hdr = b"GGUF" + struct.pack("<IQQ", 3, 2, 2)
+    hdr += s("general.architecture") + struct.pack("<I", 8) + s("qwen3")
+    hdr += s("general.alignment") + struct.pack("<II", 4, 64)
+    hdr += s("token_embd.weight") + struct.pack("<IQQIQ", 2, 64, 4, 8, 0)
+    hdr += s("output_norm.weight") + struct.pack("<IQIQ", 1, 64, 0, 320)
+    assert len(hdr) == 209
+    q8 = bytes(range(256)) + bytes(16)
+    norm = np.arange(64, dtype=np.float32).tobytes()
+    blob = hdr + bytes(256 - 209) + q8 + bytes(320 - 272) + norm
+    path = tmp_path / "hand.gguf"
+    path.write_bytes(blob)
+    want = [("token_embd.weight", (64, 4), 8, 256), ("output_norm.weight", (64,), 0, 576)]
+    assert gguf_tensor_table(path) == want
+    table, kv = og.read_table(str(path))
+    assert table == want and kv["general.architecture"] == "qwen3"
+    assert blob[576:576 + 256] == norm

@@ -5,10 +5,12 @@ the CPU in fp32 and is itself pinned by float64 finite differences
 (tests/test_oracle_engine.py).  Both sides get identical weights; for a
 quantised base the oracle receives the reference-dequantised fp32 values of the
 very bytes the engine holds.  Bar (norm-wise relative error per tensor):
-fp32 mode 1e-5; bf16 mode: loss 2e-2, whole-step gradients 3e-2.  The bf16
-whole-step bar compares a bf16 forward (q/k/v/activations rounded to bf16, as
-the MFMA path requires) with an all-fp32 reference run; each bf16 kernel on
-identical inputs is held to 2e-2 (and measures ~2e-3) in test_gpu_slots.py and
+fp32 mode 1e-5; bf16 mode 2e-2 (loss and every gradient).  The bf16 whole-step
+bar compares a bf16 forward (weights, q/k/v and activations rounded to bf16, as
+the MFMA path requires) with an all-fp32 reference run.  Those tests draw their
+weights the way the benchmark configurations do (base N(0, 0.02), LoRA A
+Kaiming-uniform, B N(0, 1e-3), norms N(1, 0.1)); each bf16 kernel on identical
+inputs is held to 2e-2 (and measures ~2e-3) in test_gpu_slots.py and
 test_gpu_flash.py.
 """
 import numpy as np
@@ -47,10 +49,14 @@ def _ocfg(c):
                             qk_norm=c.qk_norm, lora_rank=c.lora_rank, lora_alpha=c.lora_alpha)
 
 
-def build(orc, c, seed, params=None):
-    """Random weights loaded into a GPU engine and the matching oracle dicts."""
+def build(orc, c, seed, params=None, init="wide", max_grad_norm=0.0):
+    """Random weights loaded into a GPU engine and the matching oracle dicts.
+
+    init "wide": every weight N(0, 0.05) (large activations, exercises the fp32 bar);
+    init "config": the benchmark configurations' draws (base N(0, 0.02), LoRA A
+    Kaiming-uniform U(+-1/sqrt(In)), LoRA B N(0, 1e-3))."""
     rng = np.random.default_rng(seed)
-    eng = Engine(c, lr=1e-3, max_grad_norm=0.0)
+    eng = Engine(c, lr=1e-3, max_grad_norm=max_grad_norm)
     P, G = {}, {}
     for name, shape, kind in tensor_specs(c):
         if params is not None and name in params:
@@ -59,8 +65,13 @@ def build(orc, c, seed, params=None):
             w = (1 + 0.1 * rng.standard_normal(shape)).astype(np.float32)
         elif kind == "bias":
             w = (0.05 * rng.standard_normal(shape)).astype(np.float32)
-        elif kind == "lora":
-            w = (0.05 * rng.standard_normal(shape)).astype(np.float32)
+        elif kind == "lora" and init == "config":
+            if name.endswith(".A"):
+                w = (rng.uniform(-1, 1, shape) / np.sqrt(shape[0])).astype(np.float32)
+            else:
+                w = (1e-3 * rng.standard_normal(shape)).astype(np.float32)
+        elif init == "config":
+            w = (0.02 * rng.standard_normal(shape)).astype(np.float32)
         else:
             w = (0.05 * rng.standard_normal(shape)).astype(np.float32)
         if kind == "base" and c.base_qtype != QTYPE_F32:
@@ -75,8 +86,8 @@ def build(orc, c, seed, params=None):
     return eng, P, G
 
 
-def run_pair(orc, dev, c, seed=0, tol=1e-5, params=None, ids=None, loss_tol=None):
-    eng, P, G = build(orc, c, seed, params)
+def run_pair(orc, dev, c, seed=0, tol=1e-5, params=None, ids=None, loss_tol=None, init="wide"):
+    eng, P, G = build(orc, c, seed, params, init=init)
     if ids is None:
         ids = torch.from_numpy(np.random.default_rng(seed + 1).integers(0, c.vocab, c.tokens).astype(np.int32)).to(dev)
     labels = next_token_labels(ids, c.seq)
@@ -133,7 +144,7 @@ def test_engine_lora_bf16(orc, dev, qtype, base_ws, monkeypatch):
     c = ModelConfig(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=512, batch=2,
                     seq=128, rope_theta=1e6, rope_neox=1, qk_norm=1, base_qtype=qtype, lora_rank=8, lora_alpha=16.0,
                     precision=PREC_BF16)
-    run_pair(orc, dev, c, seed=7, tol=3e-2, loss_tol=2e-2)
+    run_pair(orc, dev, c, seed=7, tol=2e-2, init="config")
 
 
 def test_engine_lora_bf16_large_vocab(orc, dev):
@@ -142,13 +153,13 @@ def test_engine_lora_bf16_large_vocab(orc, dev):
     c = ModelConfig(n_layers=1, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=256, vocab=40000, batch=1,
                     seq=128, rope_theta=1e6, rope_neox=1, qk_norm=1, base_qtype=QTYPE_Q8_0, lora_rank=8,
                     lora_alpha=16.0, precision=PREC_BF16)
-    run_pair(orc, dev, c, seed=13, tol=3e-2, loss_tol=2e-2)
+    run_pair(orc, dev, c, seed=13, tol=2e-2, init="config")
 
 
 def test_engine_full_bf16(orc, dev):
     c = ModelConfig(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=512, batch=2,
                     seq=128, rope_theta=1e6, rope_neox=1, qk_norm=1, precision=PREC_BF16)
-    run_pair(orc, dev, c, seed=9, tol=3e-2, loss_tol=2e-2)
+    run_pair(orc, dev, c, seed=9, tol=2e-2, init="config")
 
 
 def test_engine_config1_tiny_llama_exact(orc, dev):

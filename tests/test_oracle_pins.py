@@ -468,3 +468,62 @@ def test_lora_forward_contract_and_backward_fd(orc):
     dB[:] = 0
     orc.orc_lora_bwd(f32(dY), f32(x), f32(W), f32(A), np.zeros((r, Out), np.float32), dA, dB, dX, T, In, Out, r, s)
     assert (dA == 0).all() and rel_err(dX, dY @ W) < 1e-6
+
+
+# ------------------------------------------------------------------ encoder known-answer blocks
+# Bytes derived by hand from TensorQuantizer.WriteBlock (TensorQuantizer.cs:80-144: d = amax/127
+# stored as (Half)d, q = Round(x/d, AwayFromZero) with the float d) and WriteKQ4 /
+# PackScaleMinK4 (TensorQuantizer.KQuant.cs:173-225, 451-459).  Each block holds values where a
+# plausible mistake gives other bytes: round-half-even or truncation of x/d, truncation of d to
+# half, dividing by the half-rounded d, the sc clamp at 1, the mn clamp at 0, mn = 63 in the packed
+# high bits, sc/mn of an upper sub-block, and the zero-range branch.
+def test_q8_0_encoder_known_blocks(orc):
+    a = np.zeros(32, np.float32)  # amax 127 -> d = 1.0 (half 0x3C00)
+    a[:7] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.4999999, -127.0]
+    b = np.zeros(32, np.float32)  # amax/127 = 1 + 3*2^-12: (Half) rounds to nearest even -> 0x3C01
+    b[0], b[1] = 127.093017578125, 99.583   # 99.583 / 1.000732421875 = 99.51 -> 100 (99 with the half d)
+    c = np.zeros(32, np.float32)  # zero block: d = 0, codes 0
+    x = np.concatenate([a, b, c])
+    raw = np.zeros(3 * 34, np.uint8)
+    assert orc.orc_quantize_q8_0(x, x.size, raw) == 0
+    ea = [0x00, 0x3C, 0x7F, 0x03, 0xFD, 0x01, 0xFF, 0x01, 0x81] + [0] * 25
+    eb = [0x01, 0x3C, 0x7F, 0x64] + [0] * 30
+    assert raw.tolist() == ea + eb + [0] * 34
+
+
+def test_q4k_encoder_known_blocks(orc):
+    # block 1: amax 63 -> step 1.0 (d = dmin = 0x3C00); per sub-block (sc, mn) by hand:
+    #   0: [-2, 28, -1, 1, 3, 0...]  range 30 -> sc 2, mn 2; codes (x+2)/2: 0, 15, 1 (0.5 away), 2, 3 (2.5 away), 1...
+    #   1: [0.1, 0...]               range 0.1 -> sc round(0.0067) = 0 -> clamp 1; mn -0 -> 0; codes 0
+    #   2: [5, 10, 7.5...]           range 5 -> sc 0 -> 1; mn round(-5) -> clamp 0; codes 5, 10, 8 (7.5 away)
+    #   3: all -3                    zero range: sc 0, mn 3, codes 0
+    #   4: [-10, 27.5, 0...]         range 37.5 -> sc round(2.5) = 3 (away), mn 10; codes 0, 13 (12.5), 3 (3.33)
+    #   5: [-63, 1, 0...]            range 64 -> sc 4, mn 63; codes 0, 15 (16 clamped), 15 (15.75 -> 16 clamped)
+    #   6: all 0                     zero range: sc 0, mn 0
+    #   7: [63, 0...]                range 63 -> sc 4, mn 0; codes 15 (15.75 -> 16 clamped), 0
+    # block 2: amax 63.046142578125 -> step 1 + 3*2^-12, half RNE 0x3C01; sub-block 0 = [amax, 0...]: sc 4, mn 0
+    blk = np.zeros((8, 32), np.float32)
+    blk[0, :5] = [-2, 28, -1, 1, 3]
+    blk[1, 0] = 0.1
+    blk[2, :] = 7.5
+    blk[2, :2] = [5, 10]
+    blk[3, :] = -3
+    blk[4, :2] = [-10, 27.5]
+    blk[5, :2] = [-63, 1]
+    blk[7, 0] = 63
+    blk2 = np.zeros(256, np.float32)
+    blk2[0] = 63.046142578125
+    x = np.concatenate([blk.ravel(), blk2])
+    raw = np.zeros(2 * 144, np.uint8)
+    assert orc.orc_quantize_q4k(x, x.size, raw) == 0
+    e1 = [0x00, 0x3C, 0x00, 0x3C]
+    e1 += [0x02, 0x01, 0x01, 0x00, 0x02, 0xC0, 0x00, 0x03, 0xA3, 0xF4, 0x00, 0x04]
+    qs = [0x01] * 128
+    qs[0:5] = [0x00, 0x0F, 0x01, 0x02, 0x03]              # sub 0 low nibbles, sub 1 high nibbles (0)
+    qs[32:64] = [0x05, 0x0A] + [0x08] * 30                 # sub 2 low, sub 3 high (0)
+    qs[64:96] = [0x00, 0xFD] + [0xF3] * 30                 # sub 4 low, sub 5 high
+    qs[96:128] = [0xF0] + [0x00] * 31                      # sub 6 low (0), sub 7 high
+    e1 += qs
+    e2 = [0x01, 0x3C, 0x01, 0x3C] + [0x04] + [0x00] * 11 + [0x0F] + [0x00] * 127
+    assert raw[:144].tolist() == e1
+    assert raw[144:].tolist() == e2
