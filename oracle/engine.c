@@ -65,8 +65,10 @@ static void lora_fwd_add(const orc_cfg* c, float** P, int l, int p, const float*
   if (!A || !Bm) return;
   int r = c->lora_rank;
   float s = c->lora_alpha / (float)r;
-  double* u = (double*)malloc(sizeof(double) * (size_t)r);
+  if (r > 256) abort(); /* the per-thread u below holds at most 256 ranks */
+#pragma omp parallel for schedule(static)
   for (int t = 0; t < T; t++) {
+    double u[256];
     for (int j = 0; j < r; j++) {
       double a = 0;
       for (int i = 0; i < In; i++) a += (double)x[(int64_t)t * In + i] * A[(int64_t)i * r + j];
@@ -78,7 +80,6 @@ static void lora_fwd_add(const orc_cfg* c, float** P, int l, int p, const float*
       y[(int64_t)t * fo + off + o] += (float)((double)s * a);
     }
   }
-  free(u);
 }
 
 /* LoRA backward of projection p: dA, dB += ; dX[T,In] += s (dY B^T) A^T */
@@ -95,6 +96,7 @@ static void lora_bwd_add(const orc_cfg* c, float** P, float** G, int l, int p, c
   double s = (double)(c->lora_alpha / (float)r);
   double* u = (double*)calloc((size_t)T * r, sizeof(double));
   double* z = (double*)calloc((size_t)T * r, sizeof(double));
+#pragma omp parallel for schedule(static)
   for (int t = 0; t < T; t++)
     for (int j = 0; j < r; j++) {
       double a = 0, b = 0;
@@ -104,6 +106,7 @@ static void lora_bwd_add(const orc_cfg* c, float** P, float** G, int l, int p, c
       z[(int64_t)t * r + j] = b;
     }
   if (dB)
+#pragma omp parallel for schedule(static)
     for (int j = 0; j < r; j++)
       for (int o = 0; o < Out; o++) {
         double a = 0;
@@ -111,12 +114,14 @@ static void lora_bwd_add(const orc_cfg* c, float** P, float** G, int l, int p, c
         dB[(int64_t)j * Out + o] += (float)(s * a);
       }
   if (dA)
+#pragma omp parallel for schedule(static)
     for (int i = 0; i < In; i++)
       for (int j = 0; j < r; j++) {
         double a = 0;
         for (int t = 0; t < T; t++) a += (double)x[(int64_t)t * In + i] * z[(int64_t)t * r + j];
         dA[(int64_t)i * r + j] += (float)(s * a);
       }
+#pragma omp parallel for schedule(static)
   for (int t = 0; t < T; t++)
     for (int i = 0; i < In; i++) {
       double a = 0;

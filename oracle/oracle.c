@@ -251,15 +251,18 @@ float orc_vecdot_q4k(const float* in, const uint8_t* raw, int col, int K) {
 }
 
 void orc_qmatmul_q8_0(const float* in, const uint8_t* raw, float* out, int M, int K, int N) {
+  #pragma omp parallel for schedule(static)
   for (int m = 0; m < M; m++)
     for (int n = 0; n < N; n++) out[(int64_t)m * N + n] = orc_vecdot_q8_0(in + (int64_t)m * K, raw, n, K);
 }
 void orc_qmatmul_q4k(const float* in, const uint8_t* raw, float* out, int M, int K, int N) {
+  #pragma omp parallel for schedule(static)
   for (int m = 0; m < M; m++)
     for (int n = 0; n < N; n++) out[(int64_t)m * N + n] = orc_vecdot_q4k(in + (int64_t)m * K, raw, n, K);
 }
 void orc_qmatmul_f32(const float* in, const float* w, float* out, int M, int K, int N) {
   /* VecDotF32 semantics: W rows [N][K]; double accumulation (QuantizationKernels.Float.cs:11-55) */
+  #pragma omp parallel for schedule(static)
   for (int m = 0; m < M; m++)
     for (int n = 0; n < N; n++) {
       double s = 0;
@@ -361,6 +364,7 @@ void orc_grad_linear(const float* dY, const float* X, const float* W, float* dW,
                      float* dX, int B, int In, int Out) {
   /* Linear_Scalar, GradientKernels.cs:50-112 */
   memset(dX, 0, sizeof(float) * (size_t)B * In);
+  #pragma omp parallel for schedule(static)
   for (int b = 0; b < B; b++)
     for (int o = 0; o < Out; o++) {
       float g = dY[(int64_t)b * Out + o];
@@ -368,13 +372,16 @@ void orc_grad_linear(const float* dY, const float* X, const float* W, float* dW,
       float* d = dX + (int64_t)b * In;
       for (int i = 0; i < In; i++) d[i] += g * w[i];
     }
-  for (int o = 0; o < Out && dW; o++) {
+  if (dW) {
+#pragma omp parallel for schedule(static)
+  for (int o = 0; o < Out; o++) {
     float* dw = dW + (int64_t)o * In;
     for (int b = 0; b < B; b++) {
       float g = dY[(int64_t)b * Out + o];
       const float* x = X + (int64_t)b * In;
       for (int i = 0; i < In; i++) dw[i] += g * x[i];
     }
+  }
   }
   if (db)
     for (int o = 0; o < Out; o++) {
@@ -436,12 +443,14 @@ void orc_grad_attention(const float* dO, const float* q, const float* k, const f
   memset(dQ, 0, sizeof(float) * (size_t)S * D);
   memset(dK, 0, sizeof(float) * (size_t)S * D);
   memset(dV, 0, sizeof(float) * (size_t)S * D);
+  #pragma omp parallel for schedule(static)
   for (int j = 0; j < S; j++)
     for (int d = 0; d < D; d++) {
       float sum = 0.f;
       for (int i = 0; i < S; i++) sum += P[(int64_t)i * S + j] * dO[(int64_t)i * D + d];
       dV[(int64_t)j * D + d] += sum;
     }
+  #pragma omp parallel for schedule(static)
   for (int i = 0; i < S; i++)
     for (int j = 0; j < S; j++) {
       float sum = 0.f;
@@ -455,6 +464,7 @@ void orc_grad_attention(const float* dO, const float* q, const float* k, const f
     for (int j = 0; j < S; j++) dot += p[j] * dp[j];
     for (int j = 0; j < S; j++) dp[j] = p[j] * (dp[j] - dot); /* dScores in place */
   }
+  #pragma omp parallel for schedule(static)
   for (int i = 0; i < S; i++)
     for (int d = 0; d < D; d++) {
       float sq = 0.f, sk = 0.f;
@@ -675,6 +685,7 @@ void orc_attention_fwd(const float* q, const float* k, const float* v, float* pr
   float scale = 1.f / sqrtf((float)D);
   int group = Hq / Hkv;
   memset(probs, 0, sizeof(float) * (size_t)B * Hq * S * S);
+  #pragma omp parallel for collapse(2) schedule(static)
   for (int b = 0; b < B; b++)
     for (int h = 0; h < Hq; h++) {
       int kvh = h / group;

@@ -228,7 +228,7 @@ def test_activation_backward(orc, dev, fn):
     assert rel_err(H(out), ref) <= FP32_TOL
 
 
-@pytest.mark.parametrize("Tn,F", [(512, 3072), (33, 1001)])
+@pytest.mark.parametrize("Tn,F", [(8192, 3072), (512, 3072), (33, 1001)])
 def test_swiglu(orc, dev, Tn, F):
     rng = np.random.default_rng(Tn + F)
     g, u, da = (f32(rng.standard_normal((Tn, F))) for _ in range(3))
@@ -258,7 +258,7 @@ def test_rope(orc, dev, neox, theta, D):
 
 
 # ------------------------------------------------------------------ loss
-@pytest.mark.parametrize("Tn,V,sm", [(256, 32000, 0.0), (64, 32000, 0.1), (8, 151936, 0.0), (40, 513, 0.0), (16, 1000, 0.2)])
+@pytest.mark.parametrize("Tn,V,sm", [(8192, 32000, 0.0), (256, 32000, 0.0), (64, 32000, 0.1), (8, 151936, 0.0), (40, 513, 0.0), (16, 1000, 0.2)])
 def test_cross_entropy(orc, dev, Tn, V, sm):
     rng = np.random.default_rng(Tn + V)
     z = f32(rng.standard_normal((Tn, V)) * 2)
@@ -289,7 +289,7 @@ def test_cross_entropy_in_place(orc, dev, Tn, V):
 
 
 # ------------------------------------------------------------------ TrainingOps
-@pytest.mark.parametrize("n", [1_000_003, 7])
+@pytest.mark.parametrize("n", [100_000_000, 1_000_003, 7])
 def test_adamw_bitexact(orc, dev, n):
     rng = np.random.default_rng(60)
     d, g = f32(rng.standard_normal(n) * 0.02), f32(rng.standard_normal(n) * 0.02)
