@@ -168,6 +168,21 @@ int smhip_flash_attention_backward(const void* q, const void* k, const void* v, 
                                    int64_t ldv, int64_t ldo, int64_t lddo, int64_t lddq,
                                    int64_t lddk, int64_t lddv, smhip_stream_t stream);
 
+/* Allocation-free variant of smhip_flash_attention_backward.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and results (bit for bit) as
+ * smhip_flash_attention_backward; the scratch it needs, B*Hq*S*(2*D+1)*4 + 256 bytes, comes from a
+ * fixed per-device array of smhip_flash_attention_backward_noalloc_limit() bytes (80 MiB) instead of
+ * the library's workspace pool, and larger problems return SMHIP_EINVAL.  The entry calls no
+ * hipMalloc/hipFree.  All calls on one device share that array: calls that overlap on one device
+ * (several streams or threads at once) race and must be serialised by the caller. */
+int smhip_flash_attention_backward_noalloc(const void* q, const void* k, const void* v, const void* o,
+                                           const void* dO, const float* lse, float* dq, float* dk, float* dv,
+                                           int B, int S, int Hq, int Hkv, int D, int64_t ldq, int64_t ldk,
+                                           int64_t ldv, int64_t ldo, int64_t lddo, int64_t lddq, int64_t lddk,
+                                           int64_t lddv, smhip_stream_t stream);
+int smhip_flash_attention_backward_noalloc_limit(int64_t* bytes);
+
 /* General dense GEMM on MFMA: C[M,N] = alpha * sum_k A(m,k) B(n,k) + beta * C.
  * Operand modes: 0 fp32 k-contiguous (X[r*ld + k]), 1 fp32 row-contiguous (X[k*ld + r]),
  * 2 bf16 k-contiguous, 3 bf16 row-contiguous.  C is fp32 (c_bf16 = 0) or bf16.  split_k > 1 splits

@@ -670,3 +670,62 @@ int smhip_flash_attention_backward(const void* q, const void* k, const void* v, 
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- allocation-free flash backward
+// For callers that cannot allocate device memory (code under HIP graph capture, tight serving
+// loops): the backward's scratch (row terms D_i and the per-query-head dK/dV partials) lives in a
+// file-scope device array instead of the workspace pool.  Each device holds its own copy; its
+// address is looked up once per device with the device current.  Calls on one device share the
+// array, so calls that overlap on one device race.
+namespace {
+constexpr size_t kNoAllocScratchBytes = (size_t)80 << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_for_current_device(void** out) {
+  int dev = 0;
+  SMHIP_CHECK_HIP(hipGetDevice(&dev));
+  SMHIP_REQUIRE(dev >= 0 && dev < kMaxDevices, "flash_attention_backward_noalloc: device index out of range");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    SMHIP_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    SMHIP_REQUIRE(p, "flash_attention_backward_noalloc: no device address for the scratch array");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SMHIP_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int smhip_flash_attention_backward_noalloc_limit(int64_t* bytes) {
+  SMHIP_REQUIRE(bytes, "flash_attention_backward_noalloc_limit: null argument");
+  *bytes = (int64_t)kNoAllocScratchBytes;
+  return SMHIP_OK;
+}
+
+int smhip_flash_attention_backward_noalloc(const void* q, const void* k, const void* v, const void* o, const void* dO,
+                                           const float* lse, float* dq, float* dk, float* dv, int B, int S, int Hq,
+                                           int Hkv, int D, int64_t ldq, int64_t ldk, int64_t ldv, int64_t ldo,
+                                           int64_t lddo, int64_t lddq, int64_t lddk, int64_t lddv,
+                                           smhip_stream_t stream) {
+  SMHIP_REQUIRE(q && k && v && o && dO && lse && dq && dk && dv && B > 0 && S > 0 && Hq > 0 && D > 0,
+                "flash_attention_backward_noalloc: bad arguments");
+  const size_t need = flash_backward_workspace(B, S, Hq, D);
+  if (need > kNoAllocScratchBytes)
+    return fail(SMHIP_EINVAL, "flash_attention_backward_noalloc: B*Hq*S*(2*D+1)*4 bytes of scratch (" +
+                                  std::to_string(need) + ") exceed the fixed " + std::to_string(kNoAllocScratchBytes) +
+                                  "-byte array; use smhip_flash_attention_backward");
+  void* ws = nullptr;
+  if (int rc = scratch_for_current_device(&ws)) return rc;
+  return flash_backward((const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)o,
+                        (const uint16_t*)dO, lse, dq, dk, dv, B, S, Hq, Hkv, D, ldq, ldk, ldv, ldo, lddo, lddq, lddk,
+                        lddv, ws, STREAM(stream));
+}
+
+}  // extern "C"
+
