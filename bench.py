@@ -10,8 +10,8 @@ labels) are already in HBM.  The step runs as a replayed HIP graph (bit-identica
 to eager launches).  The dominant kernel's roofline comes from HIP events the library
 records for each MFMA GEMM launch on its own stream (timestamped by the dispatch, via
 hipExtLaunchKernelGGL) during a separate pass of eager steps after the timed region
-(smhip_profile_begin/end).  cpu_baseline times the
-oracle's scalar C restatement of the same step on a bounded sample (see
+(smhip_profile_begin/end).  cpu_baseline times a restatement of the reference's
+AVX2/FMA CPU tiers (oracle/cpu_twin.c) on a bounded sample of the same workload (see
 cpu_baseline()).
 """
 import argparse
@@ -118,43 +118,40 @@ def gemm_dx_traffic():
     return None
 
 
-def cpu_baseline(cfg, budget_s=30.0):
-    """Time the oracle (scalar C restatement of BackpropEngine, one thread) on a bounded sample:
-    the same layer widths, vocab and adapters, one sequence of 32 tokens, with 1 and 2 layers;
-    the per-layer cost is the difference, extrapolated to cfg.n_layers (block fwd+bwd x L + head/CE)."""
-    import numpy as np
-    import oracle
-    from sharpmind_amd.model import ModelConfig, tensor_specs
+def _host_cpu():
+    """(logical CPUs, model name) of this host, from os and /proc/cpuinfo."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return os.cpu_count(), model
 
-    S = 32
-    rng = np.random.default_rng(0)
-    times = {}
-    for L in (1, 2):
-        c = ModelConfig(**{**cfg.__dict__, "n_layers": L, "batch": 1, "seq": S, "extra": {}})
-        P, G = {}, {}
-        for name, shape, kind in tensor_specs(c):
-            if kind == "norm":
-                P[name] = np.ones(shape, np.float32)
-            else:
-                P[name] = rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)
-            if (kind == "lora") if c.lora_rank else True:
-                G[name] = np.zeros(shape, np.float32)
-        oc = oracle.EngineCfg(L=L, d=c.d_model, Hq=c.n_heads, Hkv=c.n_kv_heads, D=c.head_dim, F=c.ffn_dim,
-                              V=c.vocab, B=1, S=S, eps=c.norm_eps, theta=c.rope_theta, neox=c.rope_neox,
-                              qk_norm=c.qk_norm, lora_rank=c.lora_rank, lora_alpha=c.lora_alpha)
-        ids = rng.integers(0, c.vocab, S).astype(np.int32)
-        lab = np.roll(ids, -1).astype(np.int32)
-        lab[-1] = -100
-        t0 = time.perf_counter()
-        oracle.engine_step(oc, P, G, ids, lab)
-        times[L] = time.perf_counter() - t0
-        del P, G
-    per_layer = max(times[2] - times[1], 0.0)
-    t_full = times[1] + (cfg.n_layers - 1) * per_layer
-    return {"value": S / t_full, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"oracle/engine.c scalar step (fwd+bwd), 1x{S} tokens, real widths/vocab/adapters, "
-                      f"timed at 1 and 2 layers ({times[1]:.1f}s, {times[2]:.1f}s), extrapolated to "
-                      f"{cfg.n_layers} layers; S={S} underweights the attention S^2 term (about 15-20 s of CPU work)"}
+
+def cpu_baseline(cfg):
+    """The reference's AVX2/FMA CPU tiers, restated in oracle/cpu_twin.c (-O3 -mavx2 -mfma, OpenMP over
+    the loops the reference runs in Parallel.For, on this host's cores), timed on a bounded sample:
+    one decoder block's forward + backward + AdamW at the configuration's full batch x sequence,
+    and the head (final norm, LM head through the Q8_0 table, cross-entropy, head dX) on 128
+    tokens.  Step time = n_layers x block + head x (tokens / 128); value = tokens / step time."""
+    import oracle
+    head_tokens = 128
+    full = 0 if cfg.lora_rank else 1
+    blk, head, threads = oracle.twin_time_step(cfg.d_model, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn_dim,
+                                               cfg.vocab, cfg.batch, cfg.seq, cfg.lora_rank, head_tokens, full)
+    step = cfg.n_layers * blk + head * (cfg.tokens / head_tokens)
+    ncpu, model = _host_cpu()
+    return {"value": round(cfg.tokens / step, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "host_cpus": ncpu, "cpu_model": model,
+            "sample": f"oracle/cpu_twin.c: restatement of the reference AVX2/FMA tiers (QuantizedMatMulQ8_0 FMA, "
+                      f"Linear_FMA, Attention_Scalar per batch row, AdamWUpdate_AVX2), {threads} OpenMP threads; "
+                      f"one block fwd+bwd at {cfg.batch}x{cfg.seq} tokens = {blk:.2f} s (x{cfg.n_layers} layers), "
+                      f"head + CE on {head_tokens} tokens = {head:.2f} s (x{cfg.tokens // head_tokens}); "
+                      f"extrapolated step {step:.1f} s"}
 
 
 def main():

@@ -185,3 +185,23 @@ def engine_step(cfg, params, grads, ids, labels, want_logits=False):
                            logits.ctypes.data if want_logits else None)
     assert rc == 0
     return (loss.value, logits) if want_logits else loss.value
+
+
+class TwinCfg(ctypes.Structure):
+    _fields_ = [(n, c_int) for n in ("d", "Hq", "Hkv", "D", "F", "V", "B", "S", "r", "head_tokens", "full")]
+
+
+def twin_time_step(d, Hq, Hkv, D, F, V, B, S, r, head_tokens, full=0):
+    """cpu_twin.c: (block seconds, head seconds on head_tokens tokens, threads) of the reference's
+    AVX2/FMA CPU tiers at this shape.  Measurement infrastructure for bench.py's cpu_baseline."""
+    path = os.path.join(_HERE, "libcputwin.so")
+    if not os.path.exists(path):
+        build()
+    L = ctypes.CDLL(path)
+    L.twin_time_step.restype = c_int
+    L.twin_time_step.argtypes = [ctypes.POINTER(TwinCfg), ctypes.POINTER(ctypes.c_double)]
+    out = (ctypes.c_double * 3)()
+    cfg = TwinCfg(d, Hq, Hkv, D, F, V, B, S, r, head_tokens, full)
+    if L.twin_time_step(ctypes.byref(cfg), out) != 0:
+        raise RuntimeError("twin_time_step failed")
+    return out[0], out[1], int(out[2])
