@@ -1,617 +1,12 @@
-// gemm_bf16.hip — bf16 MFMA GEMM for gfx950 (every linear of the bf16 training step).
-//
-//   C[M,N] = alpha * sum_k A(m,k) B(n,k) [+ alpha2 * sum_k A2(m,k) B2(n,k)] [+ bias] [+ R] [+ beta C]
-//
-// Block tile BM x BN x 64 with 256 threads = 4 wave64s laid out WGM x WGN; each wave owns
-// a (BM/WGM) x (BN/WGN) block of C as 32 x 32 v_mfma_f32_32x32x16_bf16 tiles.  Operands
-// live in LDS as bf16 [row][64] tiles (128-byte rows) whose 16-byte chunks are XOR-swizzled
-// by row, so one ds_read_b128 per lane (8 consecutive k of one row: the MFMA fragment)
-// is bank-conflict free.  Operand staging by mode (template parameters):
-//   BF16_K   k-contiguous bf16: buffer_load ... lds (direct global -> LDS, no registers);
-//            each lane fetches the global chunk that belongs at its swizzled LDS slot;
-//   BF16_R   row-contiguous bf16: 4 k-rows x 8 columns per thread, transposed in
-//            registers, written as 8-byte LDS quads;
-//   Q8_K / Q4K_K   frozen base rows, Q8T / Q4KT   the same values as column planes
-//            (transposed copy for dX = dY W): int8 / 4-bit codes and their fp32 scales are
-//            loaded into registers and decoded (q*d, or (sc*d)*v - mn*dmin: the exact fp32
-//            weight) and rounded once to bf16 on the way into LDS.
-// All global loads are buffer loads whose resource covers exactly the operand: a row or
-// column beyond the matrix reads 0 (or, for row-contiguous operands, unrelated values that
-// only reach C rows/columns that are never stored), so the main loop has no guards.
-// Pipelining: the next K tile's loads (DMA or registers) are issued before the current
-// tile's MFMAs; double-buffered LDS, one barrier per K tile.  When both operands are direct
-// DMA and LDS allows, a ring of ST stages keeps ST-1 tiles in flight; its barrier carries no
-// memory fence (a fence would wait for every outstanding load and drain the ring), each
-// wave instead waits with vmcnt for the one stage it needs.  Products whose output has at
-// most one 128x128 tile per CU use an 8-wave 128x128 tile (two waves per SIMD, each 64 x 32)
-// with a 3-stage ring and no split.
-// Products with a side of at most 64 (the LoRA rank GEMMs) go to the streaming kernel of
-// skinny.hip.
-// Workgroups are numbered so that each of the 8 XCDs owns a contiguous band of output
-// tiles (consecutive workgroups are dispatched round-robin over XCDs), swept in groups of 8
-// m-panels so that operand panels are reused from that XCD's L2.
-#include <hip/hip_ext.h>
-
-#include <type_traits>
-
-#include "common.hpp"
-#include "kernels.hpp"
+// gemm_bf16.hip — bf16 MFMA GEMM for gfx950: split-K epilogues, tile / split choice and the
+// operand checks of the fast path (the kernel template is in gemm_bf16.hpp, instantiated per
+// B-operand mode by gemm_bf16_m*.hip).
+#include "gemm_bf16.hpp"
 
 namespace smhip {
 namespace g3 {
 
-constexpr int BK = 64;
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void lds_void;
-constexpr uint32_t OOB = 0x80000000u;  // any offset >= this reads 0 (resources are < 2 GiB)
-
-struct Op {
-  const void* p;
-  const float* s;
-  int64_t ld;
-  int bytes;    // bytes of p covered by the buffer resource
-  int sbytes;   // bytes of s
-};
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
-}
-__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-template <int N>
-__device__ __forceinline__ void wait_vm_n() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
-// workgroup barrier without the memory fence of __syncthreads (which waits for every
-// outstanding load, i.e. drains the DMA ring); callers wait for the stage they need with
-// wait_vm_n, and LDS reads are complete because their MFMAs consumed them
-__device__ __forceinline__ void ring_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// swizzled byte offset of 16-byte chunk c (0..7) of row r in a [rows][64] bf16 tile
-__device__ __forceinline__ int sw(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
-__device__ __forceinline__ uint32_t pk(float a, float b) { return pack_bf2(a, b); }
-// element of a vector register as float: copy to a scalar first (a bit cast applied directly
-// to a vector element reads element 0)
-__device__ __forceinline__ float as_f(uint32_t w) { return __builtin_bit_cast(float, w); }
-
-// ---------------------------------------------------------------- BF16_K: direct to LDS
-// One wave instruction moves 64 x 16 B = 8 tile rows; lane l lands at LDS byte 16*l of the
-// instruction's 1 KiB block, i.e. row (l>>3), slot (l&7); it loads the global chunk whose
-// swizzled position is that slot.
-template <int ROWS, int NT>
-struct DmaLoad {
-  static constexpr int NW = NT / 64;
-  static_assert((ROWS / 8) % NW == 0, "tile rows must split evenly over the waves");
-  static constexpr int NI = ROWS / 8 / NW;  // instructions per wave per tile
-  uint32_t off[NI];
-  __amdgpu_buffer_rsrc_t rs;
-  __device__ __forceinline__ void init(const Op& o, int r0, int R) {
-    rs = rsrc(o.p, o.bytes);
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-#pragma unroll
-    for (int j = 0; j < NI; j++) {
-      const int r = (j * NW + w) * 8 + (l >> 3);
-      const int c = (l & 7) ^ ((r >> 1) & 7);
-      off[j] = (r0 + r < R) ? (uint32_t)(((int64_t)(r0 + r) * o.ld) * 2 + c * 16) : OOB;
-    }
-  }
-  __device__ __forceinline__ void fetch(uint8_t* tile, int k0) {
-    const int w = threadIdx.x >> 6;
-#if defined(__HIP_DEVICE_COMPILE__)  // the LDS address-space cast exists only in the device pass
-#pragma unroll
-    for (int j = 0; j < NI; j++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(tile + (j * NW + w) * 1024), 16, off[j] + k0 * 2, 0, 0, 0);
-#endif
-  }
-  __device__ __forceinline__ void commit(uint8_t*) {}
-};
-
-// ---------------------------------------------------------------- BF16_R: k-strided, transposed in registers
-// quad = 4 consecutive k x 8 consecutive rows; (ROWS/8)*16 quads per tile.
-template <int ROWS, int NT>
-struct RLoad {
-  static constexpr int RG = ROWS / 8;
-  static constexpr int NQ_ALL = RG * (BK / 4);
-  static constexpr int NQ = NQ_ALL >= NT ? NQ_ALL / NT : 1;
-  u32x4 v[NQ][4];
-  uint32_t off[NQ];
-  uint32_t ldb;  // bytes per k row
-  __amdgpu_buffer_rsrc_t rs;
-  __device__ __forceinline__ bool active(int q) const { return NQ_ALL >= NT || (int)threadIdx.x < NQ_ALL; }
-  __device__ __forceinline__ void init(const Op& o, int r0, int R) {
-    rs = rsrc(o.p, o.bytes);
-    ldb = (uint32_t)(o.ld * 2);
-#pragma unroll
-    for (int q = 0; q < NQ; q++) {
-      const int id = q * NT + threadIdx.x;
-      const int rg = id % RG, kq = id / RG;
-      off[q] = (uint32_t)(((int64_t)(kq * 4) * o.ld + r0 + rg * 8) * 2);
-    }
-  }
-  __device__ __forceinline__ void fetch(uint8_t*, int k0) {
-    const uint32_t kb = (uint32_t)k0 * ldb;
-#pragma unroll
-    for (int q = 0; q < NQ; q++) {
-      if (!active(q)) continue;
-#pragma unroll
-      for (int j = 0; j < 4; j++) v[q][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, off[q] + kb + j * ldb, 0, 0);
-    }
-  }
-  __device__ __forceinline__ void commit(uint8_t* tile) {
-#pragma unroll
-    for (int q = 0; q < NQ; q++) {
-      if (!active(q)) continue;
-      const int id = q * NT + threadIdx.x;
-      const int rg = id % RG, kq = id / RG;
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const int w = i >> 1, hi = i & 1;
-        auto el = [&](int j) -> uint32_t { return hi ? (v[q][j][w] >> 16) : (v[q][j][w] & 0xFFFFu); };
-        u32x2 d;
-        d[0] = el(0) | (el(1) << 16);
-        d[1] = el(2) | (el(3) << 16);
-        *reinterpret_cast<u32x2*>(tile + sw(rg * 8 + i, kq >> 1) + (kq & 1) * 8) = d;
-      }
-    }
-  }
-};
-
-// ---------------------------------------------------------------- quantised, k-contiguous in registers
-// unit = 16 consecutive k of one row (one 16-byte int8 load, or 8 bytes of 4-bit codes)
-template <int MODE, int ROWS, int NT>
-struct QLoad {
-  static constexpr int NU = ROWS * 4 / NT;
-  static_assert(NU >= 1, "quantised operand tile needs >= 64 rows");
-  static constexpr bool Q8 = MODE == SRC_Q8_K || MODE == SRC_Q8T;
-  static constexpr bool COL = MODE == SRC_Q8T || MODE == SRC_Q4KT;
-  // per-unit raw data
-  u32x4 q[NU];                 // Q8: 16 int8;  Q4K rows: 16 code bytes;  Q4KT: 8 code bytes in q.xy
-  float s[NU][COL ? 16 : 1];   // Q8 scales (one per unit for row planes, one per k for column planes)
-  float m[NU][Q8 ? 1 : (COL ? 16 : 1)];
-  uint32_t qoff[NU], soff[NU];
-  int shift[NU];
-  __amdgpu_buffer_rsrc_t rq, rsc;
-  __device__ __forceinline__ void init(const Op& o, int r0, int R) {
-    rq = rsrc(o.p, o.bytes);
-    rsc = rsrc(o.s, o.sbytes);
-#pragma unroll
-    for (int u = 0; u < NU; u++) {
-      const int id = u * NT + threadIdx.x;
-      const int r = id >> 2, kc = id & 3, row = r0 + r;
-      shift[u] = 0;
-      if (row >= R) { qoff[u] = OOB; soff[u] = OOB; continue; }
-      const int64_t e = (int64_t)row * o.ld + kc * 16;  // flat element index at k0 = 0
-      if constexpr (MODE == SRC_Q8_K) {
-        qoff[u] = (uint32_t)e;
-        soff[u] = (uint32_t)((e >> 5) * 4);
-      } else if constexpr (MODE == SRC_Q8T) {
-        qoff[u] = (uint32_t)e;
-        soff[u] = (uint32_t)(((int64_t)(row >> 5) * o.ld + kc * 16) * 4);
-      } else if constexpr (MODE == SRC_Q4K_K) {
-        // k0 is a multiple of 64 and ld of 256, so the in-super-block position of the unit
-        // shifts by k0 within a super-block: handled in fetch from the flat index
-        qoff[u] = (uint32_t)e;  // flat element index (decoded to a byte offset in fetch)
-        soff[u] = (uint32_t)((e >> 5) * 8);
-      } else {  // Q4KT
-        qoff[u] = (uint32_t)(e >> 1);
-        soff[u] = (uint32_t)(((int64_t)(row >> 5) * o.ld + kc * 16) * 8);
-      }
-    }
-  }
-  __device__ __forceinline__ void fetch(uint8_t*, int k0) {
-#pragma unroll
-    for (int u = 0; u < NU; u++) {
-      if constexpr (MODE == SRC_Q8_K) {
-        q[u] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff[u] + k0, 0, 0);
-        s[u][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, soff[u] + k0 / 8, 0, 0));
-      } else if constexpr (MODE == SRC_Q8T) {
-        q[u] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff[u] + k0, 0, 0);
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-          const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rsc, soff[u] + k0 * 4 + c * 16, 0, 0);
-#pragma unroll
-          for (int i = 0; i < 4; i++) s[u][c * 4 + i] = as_f(t[i]);
-        }
-      } else if constexpr (MODE == SRC_Q4K_K) {
-        const uint32_t e = qoff[u] == OOB ? OOB : qoff[u] + k0;
-        const uint32_t w = e & 255;
-        const uint32_t boff = e == OOB ? OOB : (e >> 8) * 128 + (w >> 6) * 32 + (w & 31);
-        shift[u] = ((w & 63) >> 5) * 4;
-        q[u] = __builtin_amdgcn_raw_buffer_load_b128(rq, boff, 0, 0);
-        const u32x2 p = __builtin_amdgcn_raw_buffer_load_b64(rsc, soff[u] + k0 / 4, 0, 0);
-        s[u][0] = as_f(p[0]);
-        m[u][0] = as_f(p[1]);
-      } else {  // Q4KT
-        const u32x2 c2 = __builtin_amdgcn_raw_buffer_load_b64(rq, qoff[u] + k0 / 2, 0, 0);
-        q[u][0] = c2[0];
-        q[u][1] = c2[1];
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-          const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rsc, soff[u] + k0 * 8 + c * 16, 0, 0);
-          s[u][2 * c] = as_f(t[0]);
-          m[u][2 * c] = as_f(t[1]);
-          s[u][2 * c + 1] = as_f(t[2]);
-          m[u][2 * c + 1] = as_f(t[3]);
-        }
-      }
-    }
-  }
-  __device__ __forceinline__ float val(int u, int i) const {
-    if constexpr (MODE == SRC_Q8_K) {
-      return (float)(int8_t)((q[u][i >> 2] >> (8 * (i & 3))) & 0xFF) * s[u][0];
-    } else if constexpr (MODE == SRC_Q8T) {
-      return (float)(int8_t)((q[u][i >> 2] >> (8 * (i & 3))) & 0xFF) * s[u][i];
-    } else if constexpr (MODE == SRC_Q4K_K) {
-      return s[u][0] * (float)((q[u][i >> 2] >> (8 * (i & 3) + shift[u])) & 0xF) - m[u][0];
-    } else {
-      return s[u][i] * (float)((q[u][i >> 3] >> (4 * (i & 7))) & 0xF) - m[u][i];
-    }
-  }
-  __device__ __forceinline__ void commit(uint8_t* tile) {
-#pragma unroll
-    for (int u = 0; u < NU; u++) {
-      const int id = u * NT + threadIdx.x;
-      const int r = id >> 2, kc = id & 3;
-      u32x4 a, b;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        a[i] = pk(val(u, 2 * i), val(u, 2 * i + 1));
-        b[i] = pk(val(u, 8 + 2 * i), val(u, 9 + 2 * i));
-      }
-      *reinterpret_cast<u32x4*>(tile + sw(r, 2 * kc)) = a;
-      *reinterpret_cast<u32x4*>(tile + sw(r, 2 * kc + 1)) = b;
-    }
-  }
-};
-
-template <int MODE, int ROWS, int NT>
-struct LoaderFor {
-  using T = typename std::conditional<
-      MODE == SRC_BF16_K, DmaLoad<ROWS, NT>,
-      typename std::conditional<MODE == SRC_BF16_R, RLoad<ROWS, NT>, QLoad<MODE, ROWS, NT>>::type>::type;
-};
-
-// ---------------------------------------------------------------- rank-extension tile (LoRA)
-// generic guarded element loads (bf16/fp32, k- or row-contiguous), K2 <= 256
-__device__ __forceinline__ float gen_elem(int mode, const Op& o, int r, int k, int R, int K) {
-  if (r >= R || k >= K) return 0.f;
-  switch (mode) {
-    case SRC_BF16_K: return bf2f(((const uint16_t*)o.p)[(int64_t)r * o.ld + k]);
-    case SRC_BF16_R: return bf2f(((const uint16_t*)o.p)[(int64_t)k * o.ld + r]);
-    case SRC_F32_K: return ((const float*)o.p)[(int64_t)r * o.ld + k];
-    default: return ((const float*)o.p)[(int64_t)k * o.ld + r];
-  }
-}
-template <int ROWS, int NT>
-__device__ __forceinline__ void gen_tile(int mode, const Op& o, int r0, int k0, int R, int K, float mult, uint8_t* lds) {
-  for (int c = threadIdx.x; c < ROWS * 8; c += NT) {
-    const int r = c >> 3, ch = c & 7;
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = mult * gen_elem(mode, o, r0 + r, k0 + ch * 8 + i, R, K);
-    u32x4 a;
-#pragma unroll
-    for (int i = 0; i < 4; i++) a[i] = pk(v[2 * i], v[2 * i + 1]);
-    *reinterpret_cast<u32x4*>(lds + sw(r, ch)) = a;
-  }
-}
-
-// Vectorised rank-extension staging for bf16 operands whose rank K2 and row length are
-// multiples of 8 with 16-byte aligned rows: whole 8-element chunks (k-contiguous) or 8 x 8
-// register transposes (row-contiguous); chunks at k >= K2 are zero.  Same values as gen_tile.
-__device__ __forceinline__ uint4 scale_bf8(uint4 v, float mult) {
-  if (mult == 1.f) return v;
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-  uint32_t o[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) o[i] = pk(mult * bf2f((uint16_t)(w[i] & 0xFFFFu)), mult * bf2f((uint16_t)(w[i] >> 16)));
-  return make_uint4(o[0], o[1], o[2], o[3]);
-}
-template <int ROWS, int NT>
-__device__ __forceinline__ void ext_tile_k(const Op& o, int r0, int k0, int R, int K, float mult, uint8_t* lds) {
-  const uint16_t* p = (const uint16_t*)o.p;
-  for (int c = threadIdx.x; c < ROWS * 8; c += NT) {
-    const int r = c >> 3, ch = c & 7, k = k0 + ch * 8;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (r0 + r < R && k < K) v = scale_bf8(*reinterpret_cast<const uint4*>(p + (int64_t)(r0 + r) * o.ld + k), mult);
-    *reinterpret_cast<uint4*>(lds + sw(r, ch)) = v;
-  }
-}
-template <int ROWS, int NT>
-__device__ __forceinline__ void ext_tile_r(const Op& o, int r0, int k0, int R, int K, float mult, uint8_t* lds) {
-  const uint16_t* p = (const uint16_t*)o.p;
-  for (int c = threadIdx.x; c < ROWS; c += NT) {  // (8-row group, 8-k chunk)
-    const int rg = c % (ROWS / 8), ch = c / (ROWS / 8), kb = k0 + ch * 8;
-    uint32_t w[8][4];
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (kb + j < K && r0 + rg * 8 < R) v = *reinterpret_cast<const uint4*>(p + (int64_t)(kb + j) * o.ld + r0 + rg * 8);
-      w[j][0] = v.x; w[j][1] = v.y; w[j][2] = v.z; w[j][3] = v.w;
-    }
-#pragma unroll
-    for (int i = 0; i < 8; i++) {  // row rg*8+i: k = kb..kb+7
-      uint32_t e[8];
-#pragma unroll
-      for (int j = 0; j < 8; j++) e[j] = (i & 1) ? (w[j][i >> 1] >> 16) : (w[j][i >> 1] & 0xFFFFu);
-      uint4 v = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16));
-      *reinterpret_cast<uint4*>(lds + sw(rg * 8 + i, ch)) = scale_bf8(v, mult);
-    }
-  }
-}
-template <int ROWS, int NT>
-__device__ __forceinline__ void ext_tile(int mode, bool vec, const Op& o, int r0, int k0, int R, int K, float mult,
-                                         uint8_t* lds) {
-  if (vec && mode == SRC_BF16_K) ext_tile_k<ROWS, NT>(o, r0, k0, R, K, mult, lds);
-  else if (vec && mode == SRC_BF16_R) ext_tile_r<ROWS, NT>(o, r0, k0, R, K, mult, lds);
-  else gen_tile<ROWS, NT>(mode, o, r0, k0, R, K, mult, lds);
-}
-
-struct Args {
-  Op A, B, A2, B2;
-  int amode2, bmode2;
-  int ext_vec;      // extension operands qualify for ext_tile_k / ext_tile_r
-  int M, N, K, K2;
-  float alpha, alpha2, beta;
-  void* C;
-  int64_t ldc;
-  const float* bias;
-  const float* R;
-  int64_t ldr;
-  int tiles_m, tiles_n;
-  int kps;          // main K tiles per split (blockIdx.y = split)
-  float* partial;   // non-null: write raw partial sums [split][M][N] instead of C
-};
-
-template <int BM, int BN, int WGM, int NW, int ST = 2>
-struct Shape {
-  static constexpr int NT = 64 * NW;
-  static constexpr int WGN = NW / WGM;
-  static constexpr int WM = BM / WGM, WN = BN / WGN;
-  static constexpr int MB = WM / 32, NB = WN / 32;
-  static constexpr int LDS = ST * (BM + BN) * 128;
-  static constexpr int OCC = LDS * 2 <= 160 * 1024 && MB * NB <= 8 && NW == 4 ? 2 : 1;
-};
-
-// Epilogue of a BM x BN tile (layout S): lane holds column (lane&31) and rows
-// (e/4)*8 + (lane>>5)*4 + e%4 of each 32x32 accumulator block.
-template <class S, bool C_BF16>
-__device__ __forceinline__ void gemm_epilogue(const Args& g, floatx16 (&acc)[S::MB][S::NB], int m0, int n0, int split) {
-  constexpr int MB = S::MB, NB = S::NB, BM = S::WM * (S::NT / 64 / S::WGN), BN = S::WN * S::WGN;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int wm = wv / S::WGN, wn = wv % S::WGN;
-  // Whole tiles take a branch-free path, one instantiation per combination of the uniform
-  // options: the general path below tests every element and is several times the code, which a
-  // workgroup runs once, from a cold instruction cache
-  if (m0 + BM <= g.M && n0 + BN <= g.N) {
-    const int r0 = m0 + wm * S::WM + (lane >> 5) * 4, c0 = n0 + wn * S::WN + (lane & 31);
-    auto store = [&](auto has_bias, auto has_r, auto has_beta) {
-#pragma unroll
-      for (int j = 0; j < NB; j++) {
-        const int col = c0 + j * 32;
-        float bv = 0.f;
-        if constexpr (decltype(has_bias)::value) bv = g.bias[col];
-#pragma unroll
-        for (int i = 0; i < MB; i++)
-#pragma unroll
-          for (int e = 0; e < 16; e++) {
-            const int64_t row = r0 + i * 32 + (e >> 2) * 8 + (e & 3);
-            float o = g.alpha * acc[i][j][e];
-            if constexpr (decltype(has_bias)::value) o = o + bv;
-            if constexpr (C_BF16) {
-              uint16_t* c = (uint16_t*)g.C + row * g.ldc + col;
-              if constexpr (decltype(has_beta)::value) o = o + g.beta * bf2f(*c);
-              *c = f2bf(o);
-            } else {
-              float* c = (float*)g.C + row * g.ldc + col;
-              if constexpr (decltype(has_r)::value) o = o + g.R[row * g.ldr + col];
-              if constexpr (decltype(has_beta)::value) o = o + g.beta * *c;
-              *c = o;
-            }
-            // one 32x32 block at a time: hoisting every block's R / C loads spills the accumulators
-            if (e == 15) __builtin_amdgcn_sched_barrier(0);
-          }
-      }
-    };
-    using T = std::true_type;
-    using F = std::false_type;
-    if (g.partial) {
-      float* p = g.partial + (int64_t)split * g.M * g.N;
-#pragma unroll
-      for (int i = 0; i < MB; i++)
-#pragma unroll
-        for (int j = 0; j < NB; j++)
-#pragma unroll
-          for (int e = 0; e < 16; e++)
-            p[(int64_t)(r0 + i * 32 + (e >> 2) * 8 + (e & 3)) * g.N + c0 + j * 32] = acc[i][j][e];
-      return;
-    }
-    const bool bias = g.bias != nullptr, r = !C_BF16 && g.R != nullptr, beta = g.beta != 0.f;
-    if (!bias && !r && !beta) store(F{}, F{}, F{});
-    else if (!bias && r && !beta) store(F{}, T{}, F{});
-    else if (!bias && !r && beta) store(F{}, F{}, T{});
-    else if (bias && !r && !beta) store(T{}, F{}, F{});
-    else if (bias && r && !beta) store(T{}, T{}, F{});
-    else if (!bias && r && beta) store(F{}, T{}, T{});
-    else if (bias && !r && beta) store(T{}, F{}, T{});
-    else store(T{}, T{}, T{});
-    return;
-  }
-#pragma unroll
-  for (int i = 0; i < MB; i++)
-#pragma unroll
-    for (int j = 0; j < NB; j++) {
-      const int col = n0 + wn * S::WN + j * 32 + (lane & 31);
-      if (col >= g.N) continue;
-      const float bv = g.bias ? g.bias[col] : 0.f;
-#pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const int row = m0 + wm * S::WM + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-        if (row >= g.M) continue;
-        if (g.partial) {
-          g.partial[((int64_t)split * g.M + row) * g.N + col] = acc[i][j][e];
-          continue;
-        }
-        float o = g.alpha * acc[i][j][e] + bv;
-        if constexpr (C_BF16) {
-          uint16_t* c = (uint16_t*)g.C + (int64_t)row * g.ldc + col;
-          if (g.beta != 0.f) o = o + g.beta * bf2f(*c);
-          *c = f2bf(o);
-        } else {
-          float* c = (float*)g.C + (int64_t)row * g.ldc + col;
-          if (g.R) o = o + g.R[(int64_t)row * g.ldr + col];
-          if (g.beta != 0.f) o = o + g.beta * *c;
-          *c = o;
-        }
-      }
-    }
-}
-
-// TAG only names the instantiation (1: the backward dX products through the frozen base, so
-// profilers can tell them from the forward GEMMs that share the code)
-template <int BM, int BN, int WGM, int NW, int AMODE, int BMODE, bool C_BF16, int ST = 2, int TAG = 0>
-__global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW, ST>::OCC)) void gemm_kernel(Args g) {
-  using S = Shape<BM, BN, WGM, NW, ST>;
-  constexpr int NT = S::NT;
-  constexpr int MB = S::MB, NB = S::NB;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[S::LDS];
-  auto sA = [&](int buf) -> uint8_t* { return smem + buf * (BM * 128); };
-  auto sB = [&](int buf) -> uint8_t* { return smem + ST * BM * 128 + buf * (BN * 128); };
-
-  const int ntiles = g.tiles_m * g.tiles_n;
-  const int wg = blockIdx.x;
-  int tile = wg;
-  if (ntiles % 8 == 0) tile = (wg % 8) * (ntiles / 8) + wg / 8;
-  constexpr int GM = 8;
-  const int group = tile / (GM * g.tiles_n);
-  const int first_m = group * GM;
-  const int gsz = min(g.tiles_m - first_m, GM);
-  const int tm = first_m + (tile % (GM * g.tiles_n)) % gsz;
-  const int tn = (tile % (GM * g.tiles_n)) / gsz;
-  const int m0 = tm * BM, n0 = tn * BN;
-
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int wm = wv / S::WGN, wn = wv % S::WGN;
-
-  floatx16 acc[MB][NB];
-#pragma unroll
-  for (int i = 0; i < MB; i++)
-#pragma unroll
-    for (int j = 0; j < NB; j++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
-
-  typename LoaderFor<AMODE, BM, NT>::T la;
-  typename LoaderFor<BMODE, BN, NT>::T lb;
-  la.init(g.A, m0, g.M);
-  lb.init(g.B, n0, g.N);
-
-  const int nk_all = g.K / BK;
-  const int split = blockIdx.y, nsplit = gridDim.y;
-  const int kt0 = split * g.kps;
-  const int nk1 = max(0, min(nk_all, kt0 + g.kps) - kt0);
-  const int nk2 = split == nsplit - 1 ? (g.K2 + BK - 1) / BK : 0;
-
-  // fragments of k-slice kk+1 are read from LDS while the MFMAs of slice kk run
-  // mid() runs once the first fragments of the tile are requested (it issues the next
-  // tile's global loads, overlapping their issue with the LDS round trip)
-  auto compute = [&](int buf, auto&& mid) {
-    const uint8_t* a = sA(buf);
-    const uint8_t* b = sB(buf);
-    bf16x8 fa[2][MB], fb[2][NB];
-    auto rd = [&](int kk, int p) {
-      const int ch = 2 * kk + (lane >> 5);
-#pragma unroll
-      for (int i = 0; i < MB; i++) fa[p][i] = *reinterpret_cast<const bf16x8*>(a + sw(wm * S::WM + i * 32 + (lane & 31), ch));
-#pragma unroll
-      for (int j = 0; j < NB; j++) fb[p][j] = *reinterpret_cast<const bf16x8*>(b + sw(wn * S::WN + j * 32 + (lane & 31), ch));
-    };
-    rd(0, 0);
-    mid();
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; kk++) {
-      // the scheduling barriers keep the two fragment sets apart: without them the reads of
-      // slice kk+1 sink below the MFMAs of slice kk into the same registers and every
-      // slice waits out a full LDS round trip
-      if (kk + 1 < BK / 16) rd(kk + 1, (kk + 1) & 1);
-      __builtin_amdgcn_sched_barrier(0);
-      const int p = kk & 1;
-#pragma unroll
-      for (int i = 0; i < MB; i++)
-#pragma unroll
-        for (int j = 0; j < NB; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[p][i], fb[p][j], acc[i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-
-  // one tile of the rank extension [A2 | B2] (K2 columns), staged with ordinary loads into
-  // stage buf, which no main tile uses until the barrier that ends the step
-  auto ext_step = [&](int buf, int t) {
-    ext_tile<BM, NT>(g.amode2, g.ext_vec != 0, g.A2, m0, t * BK, g.M, g.K2, g.alpha2, sA(buf));
-    ext_tile<BN, NT>(g.bmode2, g.ext_vec != 0, g.B2, n0, t * BK, g.N, g.K2, 1.f, sB(buf));
-    __syncthreads();
-    compute(buf, [] {});
-    __syncthreads();
-  };
-
-  if constexpr (ST > 2) {
-    // ST-stage ring (direct-to-LDS operands only): tiles t+1 .. t+ST-2 are in flight while
-    // tile t is multiplied; the barrier at the top of iteration t also frees the stage of
-    // tile t-1, which is refilled with tile t+ST-1
-    static_assert(AMODE == SRC_BF16_K && BMODE == SRC_BF16_K, "the ring stages direct-to-LDS operands only");
-    constexpr int PER = decltype(la)::NI + decltype(lb)::NI;  // DMA instructions per wave per tile
-#pragma unroll
-    for (int t = 0; t < ST - 1; t++)
-      if (t < nk1) {
-        la.fetch(sA(t), (kt0 + t) * BK);
-        lb.fetch(sB(t), (kt0 + t) * BK);
-      }
-    // the rank extension runs first, from the stage the ring fills last, while the first tiles land
-    for (int t = 0; t < nk2; t++) ext_step(ST - 1, t);
-    for (int t = 0; t < nk1; t++) {
-      if (t + ST - 2 < nk1) wait_vm_n<(ST - 2) * PER>();
-      else wait_vm();
-      ring_barrier();
-      compute(t % ST, [&] {
-        if (t + ST - 1 < nk1) {
-          const int st = (t + ST - 1) % ST;
-          la.fetch(sA(st), (kt0 + t + ST - 1) * BK);
-          lb.fetch(sB(st), (kt0 + t + ST - 1) * BK);
-        }
-      });
-    }
-  } else if (nk1 > 0) {
-    la.fetch(sA(0), kt0 * BK);
-    lb.fetch(sB(0), kt0 * BK);
-    for (int t = 0; t < nk2; t++) ext_step(1, t);  // overlaps the first tile's loads
-    la.commit(sA(0));
-    lb.commit(sB(0));
-    wait_vm();
-    __syncthreads();
-    for (int t = 0; t < nk1; t++) {
-      const int buf = t & 1;
-      const bool more = t + 1 < nk1;
-      compute(buf, [&] {
-        if (more) {
-          la.fetch(sA(buf ^ 1), (kt0 + t + 1) * BK);
-          lb.fetch(sB(buf ^ 1), (kt0 + t + 1) * BK);
-        }
-      });
-      if (more) {
-        la.commit(sA(buf ^ 1));
-        lb.commit(sB(buf ^ 1));
-      }
-      wait_vm();
-      __syncthreads();
-    }
-  }
-  if (nk1 == 0)
-    for (int t = 0; t < nk2; t++) ext_step(0, t);
-
-  gemm_epilogue<S, C_BF16>(g, acc, m0, n0, split);
-}
+thread_local hipEvent_t tl_ev0 = nullptr, tl_ev1 = nullptr;
 
 // float4 form (N % 4 == 0, ldc / ldr % 4 == 0): 4 consecutive columns per thread, the
 // partial loads of 8 splits in flight at once; sums still in ascending split order.
@@ -692,97 +87,19 @@ __global__ void splitk_epilogue_kernel(const float* __restrict__ partial, int sp
 // N = 3072: one tile per CU at M = 4096), 128x128W8 8 waves; the others 4.  64x128 and 128x64 are
 // for skinny products (LoRA rank on one side), which are bandwidth-bound: many small
 // workgroups plus split-K keep every CU streaming.
-enum TileId { T256x256 = 0, T256x128 = 1, T128x128 = 2, T256x64 = 3, T64x128 = 4, T128x64 = 5, T128x128W8 = 6, T256x192 = 7, NTILE = 8 };
-struct TileInfo { int bm, bn, occ; double eff; };
-// eff: relative MFMA throughput per CU of the tile shape (larger tiles re-read less LDS/L2)
-static const TileInfo kTiles[NTILE] = {
-    {256, 256, Shape<256, 256, 2, 8>::OCC, 1.00},  // measured 4096^3 bf16: 972 TF/s
-    {256, 128, Shape<256, 128, 2, 4>::OCC, 0.69},  //                         673
-    {128, 128, Shape<128, 128, 2, 4>::OCC, 0.88},  //                         856
-    {256, 64, Shape<256, 64, 4, 4>::OCC, 0.60},
-    {64, 128, Shape<64, 128, 1, 4>::OCC, 0.50},
-    {128, 64, Shape<128, 64, 4, 4>::OCC, 0.50},
-    {128, 128, Shape<128, 128, 2, 8>::OCC, 0.88},
-    {256, 192, Shape<256, 192, 4, 8>::OCC, 0.87},  // one tile per CU at 4096 x 3072: 840 TF/s vs 743
-};
-
-// ring depth of the direct-to-LDS 128x128 kernels: 3 stages for the 8-wave tile (one
-// workgroup per CU, so LDS is free for a deeper ring), double buffering otherwise;
-// SMHIP_GEMM_STAGES=2..4 overrides (tuning runs)
-static int ring_stages(int nw) {
-  static const int v = [] { const char* e = getenv("SMHIP_GEMM_STAGES"); return e ? atoi(e) : 0; }();
-  return v ? v : (nw == 8 ? 3 : 2);
-}
-// the main GEMM kernel of a call; under the live profiler its start and end are timestamped by
-// the dispatch itself (no marker packets around it, so no dispatch latency in the interval)
-static thread_local hipEvent_t tl_ev0 = nullptr, tl_ev1 = nullptr;
-template <typename Kern>
-static void launch_main(Kern k, const dim3& grid, const dim3& block, hipStream_t s, const Args& a) {
-  if (tl_ev0) {
-    hipExtLaunchKernelGGL(k, grid, block, 0, s, tl_ev0, tl_ev1, 0, a);
-    tl_ev0 = tl_ev1 = nullptr;
-  } else {
-    hipLaunchKernelGGL(k, grid, block, 0, s, a);
-  }
-}
-template <int BM, int BN, int WGM, int NW, int AM, int BMD, int TAG>
-static void launch_c(const Args& a, int c_bf16, int splits, hipStream_t s) {
-  const dim3 grid(a.tiles_m * a.tiles_n, splits);
-  if constexpr (AM == SRC_BF16_K && BMD == SRC_BF16_K && BM + BN <= 256) {
-    const int st = ring_stages(NW);
-    if (st == 3 || st == 4) {
-      if (c_bf16 && !a.partial) {
-        if (st == 3) launch_main(gemm_kernel<BM, BN, WGM, NW, AM, BMD, true, 3, TAG>, grid, dim3(64 * NW), s, a);
-        else launch_main(gemm_kernel<BM, BN, WGM, NW, AM, BMD, true, 4, TAG>, grid, dim3(64 * NW), s, a);
-      } else {
-        if (st == 3) launch_main(gemm_kernel<BM, BN, WGM, NW, AM, BMD, false, 3, TAG>, grid, dim3(64 * NW), s, a);
-        else launch_main(gemm_kernel<BM, BN, WGM, NW, AM, BMD, false, 4, TAG>, grid, dim3(64 * NW), s, a);
-      }
-      return;
-    }
-  }
-  if (c_bf16 && !a.partial) launch_main(gemm_kernel<BM, BN, WGM, NW, AM, BMD, true, 2, TAG>, grid, dim3(64 * NW), s, a);
-  else launch_main(gemm_kernel<BM, BN, WGM, NW, AM, BMD, false, 2, TAG>, grid, dim3(64 * NW), s, a);
-}
-
-template <int AM, int BMD, int TAG = 0>
-static void launch_tile(int tile, const Args& a, int c_bf16, int sp, hipStream_t s) {
-  switch (tile) {
-    case T256x256: launch_c<256, 256, 2, 8, AM, BMD, TAG>(a, c_bf16, sp, s); break;
-    case T256x128: launch_c<256, 128, 2, 4, AM, BMD, TAG>(a, c_bf16, sp, s); break;
-    case T128x128: launch_c<128, 128, 2, 4, AM, BMD, TAG>(a, c_bf16, sp, s); break;
-    case T256x64: launch_c<256, 64, 4, 4, AM, BMD, TAG>(a, c_bf16, sp, s); break;
-    case T64x128: launch_c<64, 128, 1, 4, AM, BMD, TAG>(a, c_bf16, sp, s); break;
-    case T128x128W8: launch_c<128, 128, 2, 8, AM, BMD, TAG>(a, c_bf16, sp, s); break;
-    case T256x192: launch_c<256, 192, 4, 8, AM, BMD, TAG>(a, c_bf16, sp, s); break;
-    default: launch_c<128, 64, 4, 4, AM, BMD, TAG>(a, c_bf16, sp, s); break;
-  }
-}
-
 static bool dispatch(int tile, const Args& a, int amode, int bmode, int c_bf16, int sp, bool dx, hipStream_t s) {
   if (amode == SRC_BF16_K) {
-    switch (bmode) {
-      case SRC_BF16_K:
-        if (dx) launch_tile<SRC_BF16_K, SRC_BF16_K, 1>(tile, a, c_bf16, sp, s);
-        else launch_tile<SRC_BF16_K, SRC_BF16_K>(tile, a, c_bf16, sp, s);
-        return true;
-      case SRC_BF16_R: launch_tile<SRC_BF16_K, SRC_BF16_R>(tile, a, c_bf16, sp, s); return true;
-      case SRC_Q8_K: launch_tile<SRC_BF16_K, SRC_Q8_K>(tile, a, c_bf16, sp, s); return true;
-      case SRC_Q8T: launch_tile<SRC_BF16_K, SRC_Q8T>(tile, a, c_bf16, sp, s); return true;
-      case SRC_Q4K_K: launch_tile<SRC_BF16_K, SRC_Q4K_K>(tile, a, c_bf16, sp, s); return true;
-      case SRC_Q4KT: launch_tile<SRC_BF16_K, SRC_Q4KT>(tile, a, c_bf16, sp, s); return true;
-      default: return false;
-    }
+    if (bmode == SRC_BF16_K) return dispatch_bf16k(tile, a, bmode, c_bf16, sp, dx, s);
+    if (bmode == SRC_BF16_R) return dispatch_bf16r(tile, a, amode, bmode, c_bf16, sp, s);
+    if (bmode == SRC_Q8_K || bmode == SRC_Q8T) return dispatch_q8(tile, a, bmode, c_bf16, sp, s);
+    if (bmode == SRC_Q4K_K || bmode == SRC_Q4KT) return dispatch_q4k(tile, a, bmode, c_bf16, sp, s);
+    return false;
   }
-  if (amode == SRC_BF16_R && bmode == SRC_BF16_R && (!c_bf16 || a.partial)) {
-    launch_tile<SRC_BF16_R, SRC_BF16_R>(tile, a, 0, sp, s);
-    return true;
-  }
+  if (amode == SRC_BF16_R && bmode == SRC_BF16_R && (!c_bf16 || a.partial))
+    return dispatch_bf16r(tile, a, amode, bmode, 0, sp, s);
   return false;
 }
 
-// pick the tile shape with the smallest estimated time: whole "rounds" of resident
-// workgroups times the per-tile work divided by the shape's efficiency
 static bool skinny(int M, int N) { return M <= 64 || N <= 64; }
 static int pick_tile(int M, int N, int splits, int bmode) {
   static const int forced = [] {  // SMHIP_GEMM_TILE=0..5 pins the tile shape (tuning runs)
