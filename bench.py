@@ -186,7 +186,7 @@ def main():
     import sharpmind_amd
     from sharpmind_amd import check
     from sharpmind_amd.engine import Engine, next_token_labels
-    from sharpmind_amd.model import PREC_BF16
+    from sharpmind_amd.model import PREC_BF16, QTYPE_Q8_0
 
     cfg, desc = make_config(args.config)
     dev = torch.device("cuda:0")
@@ -230,8 +230,13 @@ def main():
     tf = lambda fl, ms: round(fl / (ms * 1e-3) / 1e12, 2) if ms else None
     if dx_n:  # dominant kernel: the backward dX GEMMs through the frozen quantised base
         k_ms, k_n, k_fl = dx_ms, dx_n, dx_fl
-        kname = ("gemm_kernel<..., TAG 1>: backward dX = dY W through the frozen base (bf16 copy decoded "
-                 "from Q8_0 each step), bf16 MFMA")
+        if os.environ.get("SMHIP_BASE_WS") == "1" or cfg.base_qtype != QTYPE_Q8_0:
+            kname = ("gemm_kernel<..., TAG 1>: backward dX = dY W through the frozen base (bf16 copy decoded "
+                     "each step), bf16 MFMA")
+        else:
+            kname = ("gemm_q8f_kernel<128, 128, 2, 4, 4, 2, true, ..., TAG 1, ...>: backward dX = dY W through "
+                     "the frozen Q8_0 base, int8 codes and fp16 scales copied to LDS and decoded there "
+                     "(never expanded in HBM), bf16 MFMA")
     else:
         k_ms, k_n, k_fl = all_ms, all_n, all_fl
         kname = "gemm_kernel (all linears, fwd+bwd)"

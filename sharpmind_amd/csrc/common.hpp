@@ -130,6 +130,15 @@ enum SrcMode : int {
   SRC_Q8T = 8,     // int8 p[r*ld + k], fp32 scale s[(r/32)*ld + k]
   SRC_Q4KT = 9,    // 4-bit codes p[(r*ld + k)/2] (even k in the low nibble),
                    // (sc*d, mn*dmin) float pairs s[2*((r/32)*ld + k) + {0,1}]
+  // "fragment planes" of a frozen Q8_0 base (bf16 GEMM B operand only, K = ld a multiple of 64,
+  // rows a multiple of 32): int8 codes in 2048-byte blocks of 32 rows x 64 k (row-major inside),
+  // block (rb, kt) at p[(rb*(ld/64) + kt)*2048], so one K tile of 32 rows is one contiguous copy;
+  // fp16 block scales (the Q8_0 d, bit for bit) at half index rb*ld + k for SRC_Q8FT, whose rows
+  // are the In index of W[Out][In] (dX = dY W: the block runs along the rows, one scale per
+  // (k, 32 rows)), and at rb*ld + (k/64)*64 + ((k/32)%2)*32 + r%32 for SRC_Q8F (y = x W^T: the
+  // block runs along k, one scale per (row, 32 k)).
+  SRC_Q8F = 10,
+  SRC_Q8FT = 11,
 };
 
 struct Operand {

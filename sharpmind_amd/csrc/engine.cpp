@@ -50,6 +50,7 @@ struct LayerW {
   void* qraw[4] = {};        // LoRA mode: planes storage
   QuantPlanes qt[4];         // LoRA bf16 mode: column planes (transposed copy) for dX
   void* qtraw[4] = {};
+  Operand fq[4] = {}, fqt[4] = {};  // LoRA bf16 mode, Q8_0 base: fragment planes for y = x W^T and dX = dY W
   uint16_t* wb[4] = {};      // LoRA bf16 mode with the base workspace: bf16 [Out][In] and [In][Out]
   uint16_t* wbt[4] = {};
   DenseRef la[4], lb[4];     // LoRA A [In, nr], B [nr, Out]
@@ -79,6 +80,8 @@ struct Engine {
   // tensors
   DenseRef emb, norm_f;
   QuantPlanes emb_q{}, emb_qt{};
+  Operand emb_fq{}, emb_fqt{};  // fragment planes of a Q8_0 embedding (head forward / dX)
+  bool frag = false;            // bf16 LoRA over Q8_0: base GEMMs decode fragment planes in LDS
   // bf16 LoRA engines decode the frozen quantised base once per step into bf16 copies in both
   // layouts (row for y = x W^T, transposed for dX = dY W), so every base GEMM streams bf16
   // straight to LDS; without room for it the GEMMs decode the codes in their loaders
@@ -234,8 +237,15 @@ static int build(Engine* e) {
       }
       size_t fr = 0, tot = 0;
       if (hipMemGetInfo(&fr, &tot) != hipSuccess) fr = 0;
-      const char* ev = getenv("SMHIP_BASE_WS");  // SMHIP_BASE_WS=0 keeps the fused-decode GEMMs
-      e->base_ws = dims_ok && (size_t)n_all * 4 <= fr / 4 && !(ev && atoi(ev) == 0);
+      // a Q8_0 base is read as fragment planes by GEMMs that decode it in LDS, so it is never
+      // expanded in HBM; SMHIP_BASE_WS=1 instead decodes the whole base into a bf16 workspace
+      // every step (dims permitting, at most a quarter of free HBM), =0 forces the planes
+      const char* ev = getenv("SMHIP_BASE_WS");
+      bool frag_ok = qt == SMHIP_QTYPE_Q8_0 && V % 64 == 0 && d % 64 == 0;
+      for (int p = 0; p < 4; p++) frag_ok = frag_ok && e->Out[p] % 64 == 0 && e->In[p] % 64 == 0;
+      const bool want_ws = ev ? atoi(ev) != 0 : !frag_ok;
+      e->base_ws = want_ws && dims_ok && (size_t)n_all * 4 <= fr / 4;
+      e->frag = !e->base_ws && frag_ok;
     }
     if (e->base_ws) {
       auto bfbuf = [&](uint16_t** dst, int64_t n) -> int {
@@ -264,6 +274,17 @@ static int build(Engine* e) {
       e->dq_jobs = (DequantJob*)dalloc(e, sizeof(DequantJob) * jobs.size());
       if (!e->dq_jobs) return fail(SMHIP_ENOMEM, "engine: decode table");
       SMHIP_CHECK_HIP(hipMemcpy(e->dq_jobs, jobs.data(), sizeof(DequantJob) * jobs.size(), hipMemcpyHostToDevice));
+    } else if (e->frag) {  // fragment planes, both orientations
+      auto fr2 = [&](Operand* f, Operand* ft, int64_t n) -> int {
+        const size_t b = frag_planes_bytes(n);
+        f->p = dalloc(e, b);
+        ft->p = dalloc(e, b);
+        return f->p && ft->p ? SMHIP_OK : fail(SMHIP_ENOMEM, "engine: fragment planes");
+      };
+      if (int rc = fr2(&e->emb_fq, &e->emb_fqt, (int64_t)V * d)) return rc;
+      for (int l = 0; l < c.n_layers; l++)
+        for (int p = 0; p < 4; p++)
+          if (int rc = fr2(&e->L[l].fq[p], &e->L[l].fqt[p], (int64_t)e->Out[p] * e->In[p])) return rc;
     } else if (e->bf) {  // column planes for the bf16 dX GEMMs
       void* emb_t = nullptr;
       if (int rc = mk(&e->emb_qt, &emb_t, (int64_t)V * d)) return rc;
@@ -377,6 +398,7 @@ static Operand act_r(const Engine* e, const void* p, int64_t ld) {
 // weight W[Out][In] as the B operand of  y = x W^T (k = In contiguous)
 static Operand w_fwd(const Engine* e, const LayerW& w, int p) {
   if (e->base_ws) return Operand{SRC_BF16_K, w.wb[p], nullptr, e->In[p]};
+  if (e->frag) return w.fq[p];
   if (e->lora) {
     const QuantPlanes& q = w.q[p];
     return Operand{q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8_K : SRC_Q4K_K, q.qs, q.sc, e->In[p]};
@@ -386,6 +408,7 @@ static Operand w_fwd(const Engine* e, const LayerW& w, int p) {
 // weight as the B operand of  dX = dY W  (n = In, k = Out)
 static Operand w_bwd(const Engine* e, const LayerW& w, int p) {
   if (e->base_ws) return Operand{SRC_BF16_K, w.wbt[p], nullptr, e->Out[p]};
+  if (e->frag) return w.fqt[p];
   if (e->lora && e->bf) {
     const QuantPlanes& q = w.qt[p];
     return Operand{q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8T : SRC_Q4KT, q.qs, q.sc, e->Out[p]};
@@ -583,6 +606,7 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
     g.M = T; g.N = V; g.K = d;
     g.A = act_k(e, e->xnf, d);
     if (e->base_ws) g.B = Operand{SRC_BF16_K, e->emb_b, nullptr, d};
+    else if (e->frag) g.B = e->emb_fq;
     else if (e->lora) g.B = Operand{e->emb_q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8_K : SRC_Q4K_K, e->emb_q.qs, e->emb_q.sc, d};
     else g.B = e->emb.bf ? Operand{SRC_BF16_K, e->emb.bf, nullptr, d} : Operand{SRC_F32_K, e->emb.data, nullptr, d};
     g.C = e->logits; g.ldc = V;
@@ -599,6 +623,7 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
     g.M = T; g.N = d; g.K = V;
     g.A = act_k(e, e->dlogits, V);
     if (e->base_ws) g.B = Operand{SRC_BF16_K, e->emb_bt, nullptr, V};
+    else if (e->frag) g.B = e->emb_fqt;
     else if (e->lora && e->bf) g.B = Operand{e->emb_qt.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8T : SRC_Q4KT, e->emb_qt.qs, e->emb_qt.sc, V};
     else if (e->lora) g.B = Operand{e->emb_q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8_R : SRC_Q4K_R, e->emb_q.qs, e->emb_q.sc, d};
     else g.B = e->emb.bf ? Operand{SRC_BF16_R, e->emb.bf, nullptr, d} : Operand{SRC_F32_R, e->emb.data, nullptr, d};
@@ -1080,6 +1105,17 @@ static float* arena_view(const Engine* e, const DenseRef& d, int which) {
 // rebuild the column planes of row planes q (bf16 LoRA engines keep both)
 static int refresh_cols(Engine* e, const QuantPlanes* q, hipStream_t s) {
   if (!e->bf || !e->lora || e->base_ws) return SMHIP_OK;
+  if (e->frag) {
+    auto two = [&](Operand* f, Operand* ft, int rows, int cols) -> int {
+      if (int rc = make_frag_planes(*q, rows, cols, 0, const_cast<void*>(f->p), f, s)) return rc;
+      return make_frag_planes(*q, rows, cols, 1, const_cast<void*>(ft->p), ft, s);
+    };
+    if (q == &e->emb_q) return two(&e->emb_fq, &e->emb_fqt, e->c.vocab, e->c.d_model);
+    for (auto& w : e->L)
+      for (int p = 0; p < 4; p++)
+        if (q == &w.q[p]) return two(&w.fq[p], &w.fqt[p], e->Out[p], e->In[p]);
+    return fail(SMHIP_EINVAL, "engine: unknown quantised tensor");
+  }
   QuantPlanes out;
   if (q == &e->emb_q) return make_col_planes(*q, e->c.vocab, e->c.d_model, e->emb_qt.qs, &out, s);
   for (auto& w : e->L)

@@ -93,6 +93,7 @@ static bool dispatch(int tile, const Args& a, int amode, int bmode, int c_bf16, 
     if (bmode == SRC_BF16_R) return dispatch_bf16r(tile, a, amode, bmode, c_bf16, sp, s);
     if (bmode == SRC_Q8_K || bmode == SRC_Q8T) return dispatch_q8(tile, a, bmode, c_bf16, sp, s);
     if (bmode == SRC_Q4K_K || bmode == SRC_Q4KT) return dispatch_q4k(tile, a, bmode, c_bf16, sp, s);
+    if (bmode == SRC_Q8F || bmode == SRC_Q8FT) return dispatch_q8f(tile, a, bmode, c_bf16, sp, dx, s);
     return false;
   }
   if (amode == SRC_BF16_R && bmode == SRC_BF16_R && (!c_bf16 || a.partial))
@@ -138,6 +139,8 @@ static int64_t op_bytes(const Operand& o, int rows, int K, int64_t* sbytes) {
     case SRC_Q8T: *sbytes = ((int64_t)((rows - 1) / 32) * o.ld + K) * 4; return (int64_t)(rows - 1) * o.ld + K;
     case SRC_Q4K_K: *sbytes = ((int64_t)(rows - 1) * o.ld + K) / 32 * 8; return ((int64_t)(rows - 1) * o.ld + K) / 2;
     case SRC_Q4KT: *sbytes = ((int64_t)((rows - 1) / 32) * o.ld + K) * 8; return ((int64_t)(rows - 1) * o.ld + K) / 2;
+    case SRC_Q8F:
+    case SRC_Q8FT: *sbytes = (int64_t)rows * o.ld / 16; return (int64_t)rows * o.ld;
     default: return -1;
   }
 }
@@ -149,7 +152,9 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   if (g.K % BK != 0 || g.K2 > 4 * BK) return 0;
   const int am = g.A.mode, bm = g.B.mode;
   const bool a_ok = am == SRC_BF16_K || am == SRC_BF16_R;
-  const bool b_ok = bm == SRC_BF16_K || bm == SRC_BF16_R || bm == SRC_Q8_K || bm == SRC_Q8T || bm == SRC_Q4K_K || bm == SRC_Q4KT;
+  const bool frag = bm == SRC_Q8F || bm == SRC_Q8FT;
+  const bool b_ok = bm == SRC_BF16_K || bm == SRC_BF16_R || bm == SRC_Q8_K || bm == SRC_Q8T || bm == SRC_Q4K_K ||
+                    bm == SRC_Q4KT || frag;
   if (!a_ok || !b_ok) return 0;
   // a side of at most 64 (the LoRA rank products): the bandwidth-bound skinny kernel
   if (g.K2 == 0 && !g.bias && !g.R && (g.N <= 64 || g.M <= 64) && (bm == SRC_BF16_K || bm == SRC_BF16_R)) {
@@ -171,6 +176,8 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   if ((bm == SRC_Q8_K || bm == SRC_Q8T || bm == SRC_Q4KT) && g.B.ld % 32) return 0;
   if (bm == SRC_Q4K_K && g.B.ld % 256) return 0;
   if ((bm == SRC_Q8T || bm == SRC_Q4KT) && !aligned_16(g.B.s)) return 0;
+  // fragment planes: whole 32-row groups, the plane's K is the product's, A k-contiguous bf16
+  if (frag && (g.B.ld != g.K || g.N % 32 || !aligned_16(g.B.s) || am != SRC_BF16_K)) return 0;
   if (g.K2 > 0) {
     for (int m : {g.A2.mode, g.B2.mode})
       if (m != SRC_BF16_K && m != SRC_BF16_R && m != SRC_F32_K && m != SRC_F32_R) return 0;
@@ -207,7 +214,18 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   const int nk = g.K / BK;
   int sp = std::max(1, std::min(g.split_k, nk));
   int tile;
-  if (g.split_k <= 0) {
+  if (frag) {
+    // fragment-plane B: 128x128 tiles (4 MFMA waves, 4 decoder waves, 2 loader waves); split-K
+    // only to fill the machine
+    tile = T128x128;
+    const int64_t tiles = (int64_t)ceil_div(g.M, kTiles[tile].bm) * ceil_div(g.N, kTiles[tile].bn);
+    sp = 1;
+    if (g.split_k > 0) sp = std::max(1, std::min(g.split_k, nk));
+    else if (tiles < num_cus()) sp = (int)std::max<int64_t>(1, std::min<int64_t>((num_cus() + tiles - 1) / tiles, nk / 8));
+    while (sp > 1 && (int64_t)sp * g.M * g.N * 4 > ((int64_t)64 << 20)) sp--;
+    a.kps = ceil_div(nk, sp);
+    sp = ceil_div(nk, a.kps);
+  } else if (g.split_k <= 0) {
     // automatic split-K: fill the machine (2 workgroups per CU slot for skinny, bandwidth-bound
     // products), keep >= 8 (skinny: 2) K tiles per split and the partials under 64 MiB
     tile = pick_tile(g.M, g.N, 1, bm);
@@ -241,11 +259,11 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   }
   int ev0 = -1, ev1 = -1;
   if (!prof_reserve(&ev0, &ev1, &tl_ev0, &tl_ev1)) tl_ev0 = tl_ev1 = nullptr;
-  const bool ok = dispatch(tile, a, am, bm, g.c_bf16, sp, g.prof_cat == PROF_GEMM_DX, s);
+  const bool ok = dispatch(tile, a, am, bm, g.c_bf16, sp, g.prof_cat == PROF_GEMM_DX || bm == SRC_Q8FT, s);
   tl_ev0 = tl_ev1 = nullptr;
   if (!ok) return 0;
   SMHIP_CHECK_LAUNCH();
-  prof_add(g.prof_cat ? g.prof_cat : (bm == SRC_Q8T || bm == SRC_Q4KT ? PROF_GEMM_DX : PROF_GEMM), ev0, ev1,
+  prof_add(g.prof_cat ? g.prof_cat : (bm == SRC_Q8T || bm == SRC_Q4KT || bm == SRC_Q8FT ? PROF_GEMM_DX : PROF_GEMM), ev0, ev1,
            2.0 * g.M * g.N * ((double)g.K + g.K2), g.M, g.N, g.K + g.K2);
   if (sp > 1) {
     const bool v4 = g.N % 4 == 0 && g.ldc % 4 == 0 && (!g.R || g.ldr % 4 == 0) && aligned_16(g.C) &&

@@ -380,7 +380,9 @@ struct Shape {
 
 // Epilogue of a BM x BN tile (layout S): lane holds column (lane&31) and rows
 // (e/4)*8 + (lane>>5)*4 + e%4 of each 32x32 accumulator block.
-template <class S, bool C_BF16>
+// FULL: the caller guarantees whole tiles (M % BM == 0, N % BN == 0); the general path is not
+// compiled in (its register demand would otherwise shape the whole kernel's allocation)
+template <class S, bool C_BF16, bool FULL = false>
 __device__ __forceinline__ void gemm_epilogue(const Args& g, floatx16 (&acc)[S::MB][S::NB], int m0, int n0, int split) {
   constexpr int MB = S::MB, NB = S::NB, BM = S::WM * (S::NT / 64 / S::WGN), BN = S::WN * S::WGN;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -388,7 +390,7 @@ __device__ __forceinline__ void gemm_epilogue(const Args& g, floatx16 (&acc)[S::
   // Whole tiles take a branch-free path, one instantiation per combination of the uniform
   // options: the general path below tests every element and is several times the code, which a
   // workgroup runs once, from a cold instruction cache
-  if (m0 + BM <= g.M && n0 + BN <= g.N) {
+  if (FULL || (m0 + BM <= g.M && n0 + BN <= g.N)) {
     const int r0 = m0 + wm * S::WM + (lane >> 5) * 4, c0 = n0 + wn * S::WN + (lane & 31);
     auto store = [&](auto has_bias, auto has_r, auto has_beta) {
 #pragma unroll
@@ -442,6 +444,7 @@ __device__ __forceinline__ void gemm_epilogue(const Args& g, floatx16 (&acc)[S::
     else store(T{}, T{}, T{});
     return;
   }
+  if constexpr (FULL) return;
 #pragma unroll
   for (int i = 0; i < MB; i++)
 #pragma unroll
@@ -694,6 +697,7 @@ bool dispatch_bf16k(int tile, const Args& a, int bmode, int c_bf16, int sp, bool
 bool dispatch_bf16r(int tile, const Args& a, int amode, int bmode, int c_bf16, int sp, hipStream_t s);
 bool dispatch_q8(int tile, const Args& a, int bmode, int c_bf16, int sp, hipStream_t s);
 bool dispatch_q4k(int tile, const Args& a, int bmode, int c_bf16, int sp, hipStream_t s);
+bool dispatch_q8f(int tile, const Args& a, int bmode, int c_bf16, int sp, bool dx, hipStream_t s);
 
 }  // namespace g3
 }  // namespace smhip

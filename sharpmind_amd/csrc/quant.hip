@@ -194,6 +194,63 @@ int make_col_planes(const QuantPlanes& q, int rows, int cols, void* dst, QuantPl
   return SMHIP_OK;
 }
 
+// ---------------------------------------------------------------- fragment planes (Q8_0)
+// The Q8_0 base of W[rows][cols] in the order the bf16 GEMM copies it to LDS (SRC_Q8F: B = W,
+// k = cols; SRC_Q8FT: B = W^T, k = rows): 2048-byte blocks of 32 B rows x 64 k, row-major, the
+// K tiles of a 32-row group contiguous; scales as fp16 (each fp32 scale of the row planes is a
+// binary16 value, so this is exact).
+__global__ void frag_planes_q8_kernel(const int8_t* __restrict__ qs, const float* __restrict__ sc, int rows, int cols,
+                                      int trans, uint8_t* __restrict__ codes, uint16_t* __restrict__ scales) {
+  const int N = trans ? cols : rows, K = trans ? rows : cols;
+  const int64_t groups = (int64_t)N * K / 8, nsc = (int64_t)N * K / 32;
+  const int kts = K / 64;
+  for (int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; x < groups; x += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t blk = x >> 8;  // 256 eight-byte groups per block
+    const int g8 = (int)(x & 255);
+    const int64_t rb = blk / kts;
+    const int kt = (int)(blk - rb * kts);
+    const int64_t r = rb * 32 + (g8 >> 3);
+    const int64_t k0 = (int64_t)kt * 64 + (g8 & 7) * 8;
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int64_t e = trans ? (k0 + i) * cols + r : r * cols + k0 + i;
+      w[i >> 2] |= (uint32_t)(uint8_t)qs[e] << (8 * (i & 3));
+    }
+    *reinterpret_cast<uint2*>(codes + 8 * x) = make_uint2(w[0], w[1]);
+  }
+  for (int64_t y = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; y < nsc; y += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t rb = y / K;
+    const int rem = (int)(y - rb * K);
+    float v;
+    if (trans) {
+      v = sc[((int64_t)rem * cols + rb * 32) / 32];
+    } else {
+      const int kt = rem >> 6, j = (rem >> 5) & 1, rl = rem & 31;
+      v = sc[((rb * 32 + rl) * cols + kt * 64 + j * 32) / 32];
+    }
+    scales[y] = __builtin_bit_cast(uint16_t, (_Float16)v);
+  }
+}
+size_t frag_planes_bytes(int64_t n) { return (size_t)n + (size_t)n / 16; }
+int make_frag_planes(const QuantPlanes& q, int rows, int cols, int trans, void* dst, Operand* out, hipStream_t s) {
+  SMHIP_REQUIRE(q.kind == SMHIP_QTYPE_Q8_0, "fragment planes: Q8_0 only");
+  SMHIP_REQUIRE(q.n == (int64_t)rows * cols, "fragment planes: shape does not match the planes");
+  const int N = trans ? cols : rows, K = trans ? rows : cols;
+  SMHIP_REQUIRE(N % 32 == 0 && K % 64 == 0, "fragment planes: B rows must be a multiple of 32 and K of 64");
+  SMHIP_REQUIRE(((uintptr_t)dst & 255) == 0, "fragment planes: destination must be 256-byte aligned");
+  out->mode = trans ? SRC_Q8FT : SRC_Q8F;
+  out->p = dst;
+  out->s = (const float*)((char*)dst + q.n);  // fp16 scales (see SrcMode)
+  out->ld = K;
+  const int64_t groups = q.n / 8;
+  const int g = (int)std::min<int64_t>((groups + 255) / 256, (int64_t)num_cus() * 16);
+  hipLaunchKernelGGL(frag_planes_q8_kernel, dim3(g), dim3(256), 0, s, (const int8_t*)q.qs, q.sc, rows, cols, trans,
+                     (uint8_t*)dst, (uint16_t*)((char*)dst + q.n));
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
 }  // namespace smhip
 
 namespace smhip {
