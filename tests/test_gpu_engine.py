@@ -147,6 +147,15 @@ def test_engine_lora_bf16(orc, dev, qtype, base_ws, monkeypatch):
     run_pair(orc, dev, c, seed=7, tol=2e-2, init="config")
 
 
+def test_engine_lora_bf16_rank4(orc, dev):
+    """Rank 4: the fused projections' rank extensions (12, 8, 4 columns) are not multiples of 8,
+    so the Q8_0 fragment-plane GEMM stages them element-wise (its general instantiation)."""
+    c = ModelConfig(n_layers=1, d_model=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=512, batch=2,
+                    seq=128, rope_theta=1e6, rope_neox=1, qk_norm=1, base_qtype=QTYPE_Q8_0, lora_rank=4,
+                    lora_alpha=8.0, precision=PREC_BF16)
+    run_pair(orc, dev, c, seed=17, tol=2e-2, init="config")
+
+
 def test_engine_lora_bf16_large_vocab(orc, dev):
     """Vocabulary above the register-resident cross-entropy limit (the two-pass row kernel,
     bf16 output) in a LoRA bf16 step."""

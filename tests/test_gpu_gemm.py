@@ -52,10 +52,12 @@ def test_gemm_modes(dev, M, N, K, am, bm, split, c_bf16):
 
 @pytest.mark.parametrize("qtype", [8, 12])
 @pytest.mark.parametrize("trans", [0, 1])
-@pytest.mark.parametrize("M,N,K", [(300, 256, 512), (4096, 512, 256), (64, 1024, 768), (1000, 768, 256)])
+@pytest.mark.parametrize("M,N,K", [(300, 256, 512), (4096, 512, 256), (64, 1024, 768), (1000, 768, 256), (256, 256, 4096)])
 def test_qgemm_bf16(orc, dev, qtype, trans, M, N, K):
     """Dequant-fused GEMM through Q8_0 / Q4_K weights, both directions (forward rows and
-    the dX column planes), against float64 on the bf16-rounded bit-exact dequantised weights."""
+    the dX column planes; Q8_0 as fragment planes decoded in LDS), against float64 on the
+    bf16-rounded bit-exact dequantised weights.  (256, 256, 4096) has fewer output tiles than
+    CUs, so it runs split-K (fp32 partials, ordered reduction)."""
     rng = np.random.default_rng(M + N + K + qtype + trans)
     shape = (K, N) if trans else (N, K)
     w = (rng.standard_normal(shape) * 0.05).astype(np.float32).ravel()
