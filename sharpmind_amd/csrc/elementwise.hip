@@ -17,6 +17,8 @@ __device__ inline float4 ld4(const float* p) { return *reinterpret_cast<const fl
 __device__ inline void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
 // streaming (non-temporal) 16-byte accesses for data touched once per kernel
 typedef float f4v __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
 __device__ inline float4 ldnt4(const float* p) {
   const f4v v = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(p));
   return make_float4(v.x, v.y, v.z, v.w);
@@ -40,13 +42,13 @@ static int grid_for(int64_t work_items, int per_block, int max_blocks_per_cu = 8
 // One wave per row; each lane owns VEC-wide column groups, NCH groups per row.
 // xn is either given (slot form) or rebuilt as x*rinv (engine form).
 // ============================================================================
-template <int VEC, int NCH, bool FROM_X, bool HAS_DW>
-__global__ __launch_bounds__(kBlock) void rmsnorm_bwd_kernel(
+template <int VEC, int NCH, bool FROM_X, bool HAS_DW, int NW = kBlock / 64>
+__global__ __launch_bounds__(64 * NW) void rmsnorm_bwd_kernel(
     const float* __restrict__ dY, const float* __restrict__ xin, const float* __restrict__ rinv,
     const float* __restrict__ w, float* __restrict__ dX, float* __restrict__ dw_part, int T, int D,
     int accumulate, uint16_t* __restrict__ dX_bf16) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int waves = kBlock / 64;
+  constexpr int waves = NW;
   float acc[NCH][VEC];
 #pragma unroll
   for (int c = 0; c < NCH; c++)
@@ -132,7 +134,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_bwd_kernel(
         for (int v = 0; v < VEC; v++) sh[wv * D + col + v] = acc[c][v];
     }
     __syncthreads();
-    for (int d = threadIdx.x; d < D; d += kBlock) {
+    for (int d = threadIdx.x; d < D; d += 64 * NW) {
       float s = sh[d];
       for (int k = 1; k < waves; k++) s += sh[k * D + d];
       dw_part[(int64_t)blockIdx.x * D + d] = s;
@@ -174,13 +176,16 @@ template <int VEC, int NCH, bool FROM_X, bool HAS_DW>
 static int rmsnorm_bwd_launch(const float* dY, const float* x, const float* rinv, const float* w,
                               float* dw, float* dX, int T, int D, int accumulate, uint16_t* dXb,
                               hipStream_t s) {
-  int G = grid_for(T, kBlock / 64, 2);
+  // 4-wave blocks, two per CU, looping over rows (measured: one-pass grids of 4-, 8- or 16-wave
+  // blocks were no faster and multiply the dgamma partials)
+  const int nw = 4;
+  const int G = grid_for(T, kBlock / 64, 2);
   float* part = nullptr;
   size_t shm = 0;
   if (HAS_DW) {
     part = (float*)workspace(s, sizeof(float) * (size_t)G * D, 0);
     if (!part) return fail(SMHIP_ENOMEM, "rmsnorm backward: workspace");
-    shm = sizeof(float) * (kBlock / 64) * D;
+    shm = sizeof(float) * nw * D;
   }
   hipLaunchKernelGGL((rmsnorm_bwd_kernel<VEC, NCH, FROM_X, HAS_DW>), dim3(G), dim3(kBlock), shm, s,
                      dY, x, rinv, w, dX, part, T, D, accumulate, dXb);
@@ -578,14 +583,15 @@ int rope_apply(float* x, const float* cosT, const float* sinT, int B, int S, int
 // ============================================================================
 // Cross-entropy + softmax gradient (Gradients.cs:33-84), loss (CrossEntropyLoss.cs:44-104)
 // ============================================================================
-__global__ void count_labels_kernel(const int32_t* __restrict__ labels, int T, int ignoreId,
-                                    int* __restrict__ count) {
-  __shared__ int sh[kBlock];
+// labelled-row count and (below) mean loss: one 1024-thread block, fixed-order tree reductions
+__global__ __launch_bounds__(1024) void count_labels_kernel(const int32_t* __restrict__ labels, int T, int ignoreId,
+                                                            int* __restrict__ count) {
+  __shared__ int sh[1024];
   int c = 0;
-  for (int t = threadIdx.x; t < T; t += kBlock) c += labels[t] != ignoreId;
+  for (int t = threadIdx.x; t < T; t += 1024) c += labels[t] != ignoreId;
   sh[threadIdx.x] = c;
   __syncthreads();
-  for (int o = kBlock / 2; o > 0; o >>= 1) {
+  for (int o = 512; o > 0; o >>= 1) {
     if ((int)threadIdx.x < o) sh[threadIdx.x] += sh[threadIdx.x + o];
     __syncthreads();
   }
@@ -640,8 +646,12 @@ __device__ inline float block_sum(float v, float* shm) {
 }
 
 // Register-resident rows: each of NT threads holds NV4 float4 of the row; one read, one write.
-template <int NT, int NV4, typename TOut>
-__global__ __launch_bounds__(NT) void ce_rows_reg_kernel(
+// Register-resident rows: each of NT threads holds NV4 float4 of the row; one read, one write.
+// Two 1024-thread rows resident per CU (8 waves per SIMD, at most 64 registers): one row's
+// reductions overlap the other's loads and stores.  SMOOTH = label smoothing in use (a
+// separate instantiation, so the common case carries no smoothing state).
+template <int NT, int NV4, typename TOut, bool SMOOTH>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT == 1024 && !SMOOTH ? 8 : 1))) void ce_rows_reg_kernel(
     const float* __restrict__ logits, const int32_t* __restrict__ labels, TOut* __restrict__ dL,
     float* __restrict__ row_loss, const int* __restrict__ count, int T, int V, int ignoreId,
     float smoothing) {
@@ -649,6 +659,7 @@ __global__ __launch_bounds__(NT) void ce_rows_reg_kernel(
   const int real = *count;
   const float scale = real > 0 ? 1.f / (float)real : 0.f;
   const float epsOverV = smoothing / (float)V, oneMinusE = 1.f - smoothing;
+  const int c0 = threadIdx.x * 4;  // this thread's column in chunk j is c0 + j*NT*4
   for (int t = blockIdx.x; t < T; t += gridDim.x) {
     const int lab = labels[t];
     const float* z = logits + (int64_t)t * V;
@@ -659,66 +670,65 @@ __global__ __launch_bounds__(NT) void ce_rows_reg_kernel(
       continue;
     }
     const float zl = threadIdx.x == 0 ? z[lab] : 0.f;  // read before the row is overwritten (dL may alias z)
+    // buffer loads over exactly the row: columns past V read 0 and are masked to -inf, so the
+    // loop has no per-element guards
+    const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(z), (short)0, V * 4, 0x00020000);
     float4 r[NV4];
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < NV4; j++) {
-      const int c = (j * NT + threadIdx.x) * 4;
-      if (c + 3 < V) {
-        r[j] = ldnt4(z + c);
-      } else {
-        r[j].x = c < V ? z[c] : -INFINITY;
-        r[j].y = c + 1 < V ? z[c + 1] : -INFINITY;
-        r[j].z = c + 2 < V ? z[c + 2] : -INFINITY;
-        r[j].w = c + 3 < V ? z[c + 3] : -INFINITY;
-      }
+      // the buffer range check covers the vector offset only, so the chunk offset goes there too
+      const f4v q = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(rz, c0 * 4 + j * NT * 16, 0, 0));
+      const bool in = c0 < V - j * NT * 4;  // V % 4 == 0: a float4 is wholly inside the row or wholly past it
+      r[j].x = in ? q.x : -INFINITY;
+      r[j].y = in ? q.y : -INFINITY;
+      r[j].z = in ? q.z : -INFINITY;
+      r[j].w = in ? q.w : -INFINITY;
       m = fmaxf(m, fmaxf(fmaxf(r[j].x, r[j].y), fmaxf(r[j].z, r[j].w)));
     }
     m = block_max<NT>(m, shm);
     float sum = 0.f, zsum = 0.f;
 #pragma unroll
     for (int j = 0; j < NV4; j++) {
-      const int c = (j * NT + threadIdx.x) * 4;
-      if (c < V) zsum += r[j].x + (c + 1 < V ? r[j].y : 0.f) + (c + 2 < V ? r[j].z : 0.f) + (c + 3 < V ? r[j].w : 0.f);
-      r[j].x = expf(r[j].x - m);
-      r[j].y = expf(r[j].y - m);
-      r[j].z = expf(r[j].z - m);
-      r[j].w = expf(r[j].w - m);
+      if constexpr (SMOOTH) {
+        if (c0 < V - j * NT * 4) zsum += (r[j].x + r[j].y) + (r[j].z + r[j].w);
+      }
+      r[j].x = __expf(r[j].x - m);
+      r[j].y = __expf(r[j].y - m);
+      r[j].z = __expf(r[j].z - m);
+      r[j].w = __expf(r[j].w - m);
       sum += (r[j].x + r[j].y) + (r[j].z + r[j].w);
     }
     sum = block_sum<NT>(sum, shm + NT / 64);
-    if (smoothing > 0.f) zsum = block_sum<NT>(zsum, shm + NT / 64 + NT / 64);
+    if constexpr (SMOOTH) zsum = block_sum<NT>(zsum, shm + NT / 64 + NT / 64);
     const float inv = 1.f / sum;
+    // V % 4 == 0: every float4 is wholly inside or wholly past the row
 #pragma unroll
     for (int j = 0; j < NV4; j++) {
-      const int c = (j * NT + threadIdx.x) * 4;
-      float e[4] = {r[j].x, r[j].y, r[j].z, r[j].w};
+      float e[4] = {r[j].x * inv, r[j].y * inv, r[j].z * inv, r[j].w * inv};
+      if constexpr (SMOOTH) {
 #pragma unroll
-      for (int v = 0; v < 4; v++) {
-        if (c + v < V) {
-          float p = e[v] * inv;
-          if (smoothing > 0.f) {
-            p -= epsOverV;
-            if (c + v == lab) p -= oneMinusE;
-          } else if (c + v == lab) {
-            p -= 1.f;
-          }
-          e[v] = p * scale;
-        }
+        for (int v = 0; v < 4; v++) e[v] -= epsOverV;
       }
-      if constexpr (sizeof(TOut) == 4) {
-        if (c + 3 < V) {
-          stnt4((float*)(d + c), make_float4(e[0], e[1], e[2], e[3]));
-        } else {
-          for (int v = 0; v < 4; v++) if (c + v < V) d[c + v] = e[v];
-        }
-      } else {
-        for (int v = 0; v < 4; v++) if (c + v < V) store_out(d + c + v, e[v]);
+#pragma unroll
+      for (int v = 0; v < 4; v++) e[v] *= scale;
+      if (c0 < V - j * NT * 4) {
+        if constexpr (sizeof(TOut) == 4) stnt4((float*)(d + c0 + j * NT * 4), make_float4(e[0], e[1], e[2], e[3]));
+        else *reinterpret_cast<uint2*>(d + c0 + j * NT * 4) = make_uint2(pack_bf2(e[0], e[1]), pack_bf2(e[2], e[3]));
       }
+    }
+    // the label column, rewritten by thread 0 after the row's stores have completed (same
+    // operations in the same order as the other columns, plus the one-hot term)
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float p = __expf(zl - m) * inv;
+      if constexpr (SMOOTH) p -= epsOverV;
+      p -= SMOOTH ? oneMinusE : 1.f;
+      store_out(d + lab, p * scale);
     }
     if (threadIdx.x == 0 && row_loss) {
       float lp = (zl - m) - logf(sum);
-      if (smoothing <= 0.f) {
+      if constexpr (!SMOOTH) {
         row_loss[t] = -lp;
       } else {
         float slp = zsum - (float)V * m - (float)V * logf(sum);
@@ -857,14 +867,14 @@ __global__ __launch_bounds__(NT) void ce_rows_2pass_vec_kernel(
   }
 }
 
-__global__ void mean_loss_kernel(const float* __restrict__ row_loss, const int* __restrict__ count,
-                                 int T, float* __restrict__ out) {
-  __shared__ double sh[kBlock];
+__global__ __launch_bounds__(1024) void mean_loss_kernel(const float* __restrict__ row_loss, const int* __restrict__ count,
+                                                         int T, float* __restrict__ out) {
+  __shared__ double sh[1024];
   double a = 0.0;
-  for (int t = threadIdx.x; t < T; t += kBlock) a += (double)row_loss[t];
+  for (int t = threadIdx.x; t < T; t += 1024) a += (double)row_loss[t];
   sh[threadIdx.x] = a;
   __syncthreads();
-  for (int o = kBlock / 2; o > 0; o >>= 1) {
+  for (int o = 512; o > 0; o >>= 1) {
     if ((int)threadIdx.x < o) sh[threadIdx.x] += sh[threadIdx.x + o];
     __syncthreads();
   }
@@ -879,20 +889,24 @@ static int ce_launch(const float* logits, const int32_t* labels, TOut* dL, float
   if (!ws) return fail(SMHIP_ENOMEM, "cross entropy: workspace");
   int* count = (int*)ws;
   float* row_loss = (float*)(ws + 256);
-  hipLaunchKernelGGL(count_labels_kernel, dim3(1), dim3(kBlock), 0, s, labels, T, ignoreId, count);
+  hipLaunchKernelGGL(count_labels_kernel, dim3(1), dim3(1024), 0, s, labels, T, ignoreId, count);
   int G = grid_for(T, 1, 2);
   const bool v4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dL % 16 == 0);
-  if (v4 && V <= 1024 * 4 * 8 && V > 256 * 4 * 8)
-    hipLaunchKernelGGL((ce_rows_reg_kernel<1024, 8, TOut>), dim3(G), dim3(1024), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
-  else if (v4 && V <= 256 * 4 * 8)
-    hipLaunchKernelGGL((ce_rows_reg_kernel<256, 8, TOut>), dim3(G), dim3(256), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
+  const bool sm = smoothing > 0.f;
+  if (v4 && V <= 1024 * 4 * 8 && V > 256 * 4 * 8) {
+    if (sm) hipLaunchKernelGGL((ce_rows_reg_kernel<1024, 8, TOut, true>), dim3(G), dim3(1024), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
+    else hipLaunchKernelGGL((ce_rows_reg_kernel<1024, 8, TOut, false>), dim3(G), dim3(1024), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
+  } else if (v4 && V <= 256 * 4 * 8) {
+    if (sm) hipLaunchKernelGGL((ce_rows_reg_kernel<256, 8, TOut, true>), dim3(G), dim3(256), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
+    else hipLaunchKernelGGL((ce_rows_reg_kernel<256, 8, TOut, false>), dim3(G), dim3(256), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
+  }
   else if (v4)
     hipLaunchKernelGGL((ce_rows_2pass_vec_kernel<1024, TOut>), dim3(G), dim3(1024), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
   else
     hipLaunchKernelGGL((ce_rows_2pass_kernel<1024, TOut>), dim3(G), dim3(1024), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
   SMHIP_CHECK_LAUNCH();
   if (loss) {
-    hipLaunchKernelGGL(mean_loss_kernel, dim3(1), dim3(kBlock), 0, s, row_loss, count, T, loss);
+    hipLaunchKernelGGL(mean_loss_kernel, dim3(1), dim3(1024), 0, s, row_loss, count, T, loss);
     SMHIP_CHECK_LAUNCH();
   }
   return SMHIP_OK;
@@ -919,39 +933,49 @@ __device__ inline void adam_one(float& d, float g, float& m, float& v, float b1,
   d = d - lr * (mhat / (sqrtf(vhat) + eps) + decay * d);
 }
 
+// One float4 of each stream per thread and no grid-stride loop (one pass over the grid), with
+// non-temporal loads and stores: measured on MI355X at about 5.9 TB/s for this 4-in / 3-out
+// pattern against 5.2-5.6 TB/s for grid-stride forms.
+__global__ __launch_bounds__(kBlock) void adamw_vec_kernel(float* __restrict__ data, const float* __restrict__ grad,
+                                                           float* __restrict__ m, float* __restrict__ v,
+                                                           int64_t n4, float b1, float b2, float bc1,
+                                                           float bc2, float lr, float eps, float decay) {
+  const float omb1 = 1.f - b1, omb2 = 1.f - b2;
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= n4) return;
+  float4 d = ldnt4(data + 4 * i), g = ldnt4(grad + 4 * i), mm = ldnt4(m + 4 * i), vv = ldnt4(v + 4 * i);
+  adam_one(d.x, g.x, mm.x, vv.x, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
+  adam_one(d.y, g.y, mm.y, vv.y, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
+  adam_one(d.z, g.z, mm.z, vv.z, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
+  adam_one(d.w, g.w, mm.w, vv.w, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
+  stnt4(m + 4 * i, mm);
+  stnt4(v + 4 * i, vv);
+  stnt4(data + 4 * i, d);
+}
 __global__ __launch_bounds__(kBlock) void adamw_kernel(float* __restrict__ data, const float* __restrict__ grad,
                                                        float* __restrict__ m, float* __restrict__ v,
-                                                       int64_t n, float b1, float b2, float bc1,
-                                                       float bc2, float lr, float eps, float decay,
-                                                       int vec) {
+                                                       int64_t i0, int64_t n, float b1, float b2, float bc1,
+                                                       float bc2, float lr, float eps, float decay) {
   const float omb1 = 1.f - b1, omb2 = 1.f - b2;
-  if (vec) {
-    const int64_t n4 = n / 4;
-    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += (int64_t)gridDim.x * kBlock) {
-      float4 d = ldnt4(data + 4 * i), g = ldnt4(grad + 4 * i), mm = ldnt4(m + 4 * i), vv = ldnt4(v + 4 * i);
-      adam_one(d.x, g.x, mm.x, vv.x, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
-      adam_one(d.y, g.y, mm.y, vv.y, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
-      adam_one(d.z, g.z, mm.z, vv.z, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
-      adam_one(d.w, g.w, mm.w, vv.w, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
-      stnt4(m + 4 * i, mm);
-      stnt4(v + 4 * i, vv);
-      stnt4(data + 4 * i, d);
-    }
-    for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
-      adam_one(data[i], grad[i], m[i], v[i], b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
-  } else {
-    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
-      adam_one(data[i], grad[i], m[i], v[i], b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
-  }
+  for (int64_t i = i0 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
+    adam_one(data[i], grad[i], m[i], v[i], b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
 }
 
 int adamw_update(float* data, const float* grad, float* m, float* v, int64_t n, float b1, float b2,
                  float bc1, float bc2, float lr, float eps, float decay, hipStream_t s) {
   if (n <= 0) return SMHIP_OK;
-  int vec = ((uintptr_t)data | (uintptr_t)grad | (uintptr_t)m | (uintptr_t)v) % 16 == 0;
-  hipLaunchKernelGGL(adamw_kernel, dim3(grid_for(vec ? n / 4 + 1 : n, kBlock, 4)), dim3(kBlock), 0,
-                     s, data, grad, m, v, n, b1, b2, bc1, bc2, lr, eps, decay, vec);
-  SMHIP_CHECK_LAUNCH();
+  const bool vec = ((uintptr_t)data | (uintptr_t)grad | (uintptr_t)m | (uintptr_t)v) % 16 == 0;
+  const int64_t n4 = vec ? n / 4 : 0;
+  if (n4 > 0) {
+    hipLaunchKernelGGL(adamw_vec_kernel, dim3((unsigned)((n4 + kBlock - 1) / kBlock)), dim3(kBlock), 0, s, data, grad,
+                       m, v, n4, b1, b2, bc1, bc2, lr, eps, decay);
+    SMHIP_CHECK_LAUNCH();
+  }
+  if (4 * n4 < n) {  // tail (or unaligned arrays): element-wise
+    hipLaunchKernelGGL(adamw_kernel, dim3(grid_for(n - 4 * n4, kBlock, 4)), dim3(kBlock), 0, s, data, grad, m, v,
+                       4 * n4, n, b1, b2, bc1, bc2, lr, eps, decay);
+    SMHIP_CHECK_LAUNCH();
+  }
   return SMHIP_OK;
 }
 
