@@ -313,9 +313,9 @@ int smhip_qgemm_bf16(int qtype, int trans_w, int M, int N, int K, const void* A,
   g.M = M; g.N = N; g.K = K;
   g.A = {SRC_BF16_K, A, nullptr, lda};
   g.C = C; g.ldc = ldc;
-  if (qtype == SMHIP_QTYPE_Q8_0) {
+  if (K % 64 == 0 && N % 32 == 0) {
     // fragment planes: the GEMM copies codes and scales to LDS and decodes there
-    void* fr = workspace(s, frag_planes_bytes(n), 8);
+    void* fr = workspace(s, frag_planes_bytes(n, qtype), 8);
     if (!fr) return fail(SMHIP_ENOMEM, "qgemm_bf16: workspace");
     if (int rc = make_frag_planes(qp, trans_w ? K : N, trans_w ? N : K, trans_w, fr, &g.B, s)) return rc;
   } else if (!trans_w) {

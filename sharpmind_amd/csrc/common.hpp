@@ -139,6 +139,12 @@ enum SrcMode : int {
   // block runs along k, one scale per (row, 32 k)).
   SRC_Q8F = 10,
   SRC_Q8FT = 11,
+  // Q4_K fragment planes: the same 32 x 64 blocks with 4-bit codes (1024 bytes, 32 per row;
+  // byte i of a row's dword j holds k = 8j + i in its low nibble and k = 8j + i + 4 in its high
+  // nibble) and (sc*d, mn*dmin) fp32 pairs at pair index rb*ld + k (SRC_Q4FT, blocks along the
+  // rows) or rb*ld + (k/64)*64 + ((k/32)%2)*32 + r%32 (SRC_Q4F, blocks along k).
+  SRC_Q4F = 12,
+  SRC_Q4FT = 13,
 };
 
 struct Operand {

@@ -50,7 +50,7 @@ struct LayerW {
   void* qraw[4] = {};        // LoRA mode: planes storage
   QuantPlanes qt[4];         // LoRA bf16 mode: column planes (transposed copy) for dX
   void* qtraw[4] = {};
-  Operand fq[4] = {}, fqt[4] = {};  // LoRA bf16 mode, Q8_0 base: fragment planes for y = x W^T and dX = dY W
+  Operand fq[4] = {}, fqt[4] = {};  // LoRA bf16 mode: fragment planes for y = x W^T and dX = dY W
   uint16_t* wb[4] = {};      // LoRA bf16 mode with the base workspace: bf16 [Out][In] and [In][Out]
   uint16_t* wbt[4] = {};
   DenseRef la[4], lb[4];     // LoRA A [In, nr], B [nr, Out]
@@ -80,8 +80,8 @@ struct Engine {
   // tensors
   DenseRef emb, norm_f;
   QuantPlanes emb_q{}, emb_qt{};
-  Operand emb_fq{}, emb_fqt{};  // fragment planes of a Q8_0 embedding (head forward / dX)
-  bool frag = false;            // bf16 LoRA over Q8_0: base GEMMs decode fragment planes in LDS
+  Operand emb_fq{}, emb_fqt{};  // fragment planes of the quantised embedding (head forward / dX)
+  bool frag = false;            // bf16 LoRA: base GEMMs decode fragment planes in LDS
   // bf16 LoRA engines decode the frozen quantised base once per step into bf16 copies in both
   // layouts (row for y = x W^T, transposed for dX = dY W), so every base GEMM streams bf16
   // straight to LDS; without room for it the GEMMs decode the codes in their loaders
@@ -237,11 +237,11 @@ static int build(Engine* e) {
       }
       size_t fr = 0, tot = 0;
       if (hipMemGetInfo(&fr, &tot) != hipSuccess) fr = 0;
-      // a Q8_0 base is read as fragment planes by GEMMs that decode it in LDS, so it is never
+      // a Q8_0 / Q4_K base is read as fragment planes by GEMMs that decode it in LDS, so it is never
       // expanded in HBM; SMHIP_BASE_WS=1 instead decodes the whole base into a bf16 workspace
       // every step (dims permitting, at most a quarter of free HBM), =0 forces the planes
       const char* ev = getenv("SMHIP_BASE_WS");
-      bool frag_ok = qt == SMHIP_QTYPE_Q8_0 && V % 64 == 0 && d % 64 == 0;
+      bool frag_ok = V % 64 == 0 && d % 64 == 0;
       for (int p = 0; p < 4; p++) frag_ok = frag_ok && e->Out[p] % 64 == 0 && e->In[p] % 64 == 0;
       const bool want_ws = ev ? atoi(ev) != 0 : !frag_ok;
       e->base_ws = want_ws && dims_ok && (size_t)n_all * 4 <= fr / 4;
@@ -276,7 +276,7 @@ static int build(Engine* e) {
       SMHIP_CHECK_HIP(hipMemcpy(e->dq_jobs, jobs.data(), sizeof(DequantJob) * jobs.size(), hipMemcpyHostToDevice));
     } else if (e->frag) {  // fragment planes, both orientations
       auto fr2 = [&](Operand* f, Operand* ft, int64_t n) -> int {
-        const size_t b = frag_planes_bytes(n);
+        const size_t b = frag_planes_bytes(n, qt);
         f->p = dalloc(e, b);
         ft->p = dalloc(e, b);
         return f->p && ft->p ? SMHIP_OK : fail(SMHIP_ENOMEM, "engine: fragment planes");

@@ -93,7 +93,8 @@ static bool dispatch(int tile, const Args& a, int amode, int bmode, int c_bf16, 
     if (bmode == SRC_BF16_R) return dispatch_bf16r(tile, a, amode, bmode, c_bf16, sp, s);
     if (bmode == SRC_Q8_K || bmode == SRC_Q8T) return dispatch_q8(tile, a, bmode, c_bf16, sp, s);
     if (bmode == SRC_Q4K_K || bmode == SRC_Q4KT) return dispatch_q4k(tile, a, bmode, c_bf16, sp, s);
-    if (bmode == SRC_Q8F || bmode == SRC_Q8FT) return dispatch_q8f(tile, a, bmode, c_bf16, sp, dx, s);
+    if (bmode == SRC_Q8F || bmode == SRC_Q8FT || bmode == SRC_Q4F || bmode == SRC_Q4FT)
+      return dispatch_q8f(tile, a, bmode, c_bf16, sp, dx, s);
     return false;
   }
   if (amode == SRC_BF16_R && bmode == SRC_BF16_R && (!c_bf16 || a.partial))
@@ -141,6 +142,8 @@ static int64_t op_bytes(const Operand& o, int rows, int K, int64_t* sbytes) {
     case SRC_Q4KT: *sbytes = ((int64_t)((rows - 1) / 32) * o.ld + K) * 8; return ((int64_t)(rows - 1) * o.ld + K) / 2;
     case SRC_Q8F:
     case SRC_Q8FT: *sbytes = (int64_t)rows * o.ld / 16; return (int64_t)rows * o.ld;
+    case SRC_Q4F:
+    case SRC_Q4FT: *sbytes = (int64_t)rows * o.ld / 4; return (int64_t)rows * o.ld / 2;
     default: return -1;
   }
 }
@@ -152,7 +155,7 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   if (g.K % BK != 0 || g.K2 > 4 * BK) return 0;
   const int am = g.A.mode, bm = g.B.mode;
   const bool a_ok = am == SRC_BF16_K || am == SRC_BF16_R;
-  const bool frag = bm == SRC_Q8F || bm == SRC_Q8FT;
+  const bool frag = bm == SRC_Q8F || bm == SRC_Q8FT || bm == SRC_Q4F || bm == SRC_Q4FT;
   const bool b_ok = bm == SRC_BF16_K || bm == SRC_BF16_R || bm == SRC_Q8_K || bm == SRC_Q8T || bm == SRC_Q4K_K ||
                     bm == SRC_Q4KT || frag;
   if (!a_ok || !b_ok) return 0;
@@ -259,11 +262,11 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   }
   int ev0 = -1, ev1 = -1;
   if (!prof_reserve(&ev0, &ev1, &tl_ev0, &tl_ev1)) tl_ev0 = tl_ev1 = nullptr;
-  const bool ok = dispatch(tile, a, am, bm, g.c_bf16, sp, g.prof_cat == PROF_GEMM_DX || bm == SRC_Q8FT, s);
+  const bool ok = dispatch(tile, a, am, bm, g.c_bf16, sp, g.prof_cat == PROF_GEMM_DX || bm == SRC_Q8FT || bm == SRC_Q4FT, s);
   tl_ev0 = tl_ev1 = nullptr;
   if (!ok) return 0;
   SMHIP_CHECK_LAUNCH();
-  prof_add(g.prof_cat ? g.prof_cat : (bm == SRC_Q8T || bm == SRC_Q4KT || bm == SRC_Q8FT ? PROF_GEMM_DX : PROF_GEMM), ev0, ev1,
+  prof_add(g.prof_cat ? g.prof_cat : (bm == SRC_Q8T || bm == SRC_Q4KT || bm == SRC_Q8FT || bm == SRC_Q4FT ? PROF_GEMM_DX : PROF_GEMM), ev0, ev1,
            2.0 * g.M * g.N * ((double)g.K + g.K2), g.M, g.N, g.K + g.K2);
   if (sp > 1) {
     const bool v4 = g.N % 4 == 0 && g.ldc % 4 == 0 && (!g.R || g.ldr % 4 == 0) && aligned_16(g.C) &&

@@ -416,7 +416,7 @@ __device__ __forceinline__ void gemm_epilogue(const Args& g, floatx16 (&acc)[S::
               *c = o;
             }
             // one 32x32 block at a time: hoisting every block's R / C loads spills the accumulators
-            if (e == 15) __builtin_amdgcn_sched_barrier(0);
+            if ((e & 3) == 3) __builtin_amdgcn_sched_barrier(0);
           }
       }
     };

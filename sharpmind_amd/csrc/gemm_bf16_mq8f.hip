@@ -167,13 +167,114 @@ __device__ __forceinline__ void ext_stage(int mode, const Op& o, int r0, int k0,
   else ext_tile_r<ROWS, NT>(o, r0, k0, R, K, mult, lds);
 }
 
-template <int BM, int BN, int WGM, int NWM, int NWD, int NWL, bool TRANS, bool C_BF16, int ST, int TAG, bool FULL, bool GEN>
+// Q4_K fragment planes: raw stage = BN*32 code bytes (32 per row of a 32 x 64 block) and BN*16
+// bytes of (sc*d, mn*dmin) fp32 pairs (512 bytes per 32 B rows).  A decode unit is one code
+// dword (8 consecutive k of a row: low nibbles k..k+3, high nibbles k+4..k+7); the weight is
+// fma(sc*d, v, -mn*dmin), one rounding of the exact (sc*d)*v - mn*dmin, which is the value the
+// reference forms.
+template <int BN, int NWL, int NWD, bool TRANS>
+struct FragQ4 {
+  static constexpr int NW = NWL;
+  static constexpr int NC = BN / 32;  // 1 KiB code copies per tile (one per 32 B rows)
+  static_assert(NC % NW == 0, "code copies must split evenly over the waves");
+  static constexpr int NI = NC / NW;
+  static constexpr int CODE = BN * 32;
+  static constexpr int NS = BN / 64;  // 1 KiB pair copies per tile
+  static_assert(NS % NW == 0, "pair copies must split evenly over the waves");
+  static constexpr int NIS = NS / NW;
+  static constexpr int STAGE = CODE + BN * 16;
+  static constexpr int PER = NI + NIS;
+  static constexpr int UPT = BN * 8 / (64 * NWD);
+  static_assert(UPT >= 1 && UPT <= 8, "decode units per thread");
+  uint32_t coff[NI], soff[NIS];
+  __amdgpu_buffer_rsrc_t rc, rs;
+  struct Raw {
+    uint32_t c;
+    u32x4 s[4];  // TRANS: 8 (s, m) pairs; otherwise one pair in s[0].xy
+  };
+  __device__ __forceinline__ void init(const Op& o, int n0, int N, int p) {
+    rc = rsrc(o.p, o.bytes);
+    rs = rsrc(o.s, o.sbytes);
+    const int w = p >> 6, l = p & 63;
+    const int K = (int)o.ld;
+#pragma unroll
+    for (int j = 0; j < NI; j++) {
+      const int nb = n0 / 32 + j * NW + w;
+      coff[j] = nb < N / 32 ? (uint32_t)((int64_t)nb * (K / 64) * 1024 + l * 16) : OOB;
+    }
+#pragma unroll
+    for (int j = 0; j < NIS; j++) {
+      const int b = (j * NW + w) * 1024 + l * 16, nb = n0 / 32 + b / 512;
+      soff[j] = nb < N / 32 ? (uint32_t)((int64_t)nb * K * 8 + (b & 511)) : OOB;
+    }
+  }
+  __device__ __forceinline__ void fetch(uint8_t* st, int k0, int p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const int w = p >> 6;
+#pragma unroll
+    for (int j = 0; j < NI; j++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (lds_void*)(st + (j * NW + w) * 1024), 16, coff[j] + k0 * 16, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < NIS; j++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(st + CODE + (j * NW + w) * 1024), 16, soff[j] + k0 * 8, 0, 0, 0);
+#endif
+  }
+  __device__ __forceinline__ Raw read(const uint8_t* st, int j, int p) const {
+    const int w = p >> 6, l = p & 63;
+    const int g = j * NWD + w, nbl = g >> 2, ch = l & 7;
+    Raw r;
+    r.c = *reinterpret_cast<const uint32_t*>(st + g * 256 + l * 4);
+    if constexpr (TRANS) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) r.s[i] = *reinterpret_cast<const u32x4*>(st + CODE + nbl * 512 + ch * 64 + i * 16);
+    } else {
+      const u32x2 pr = *reinterpret_cast<const u32x2*>(st + CODE + nbl * 512 + ((ch >> 2) * 32 + (g & 3) * 8 + (l >> 3)) * 8);
+      r.s[0][0] = pr[0];
+      r.s[0][1] = pr[1];
+    }
+    return r;
+  }
+  __device__ __forceinline__ void write(const Raw& r, uint8_t* bf, int j, int p) const {
+    const int w = p >> 6, l = p & 63;
+    const int g = j * NWD + w;
+    const uint32_t lo = r.c & 0x0F0F0F0Fu, hi = (r.c >> 4) & 0x0F0F0F0Fu;
+    const float v[8] = {(float)(lo & 0xFFu), (float)((lo >> 8) & 0xFFu), (float)((lo >> 16) & 0xFFu), (float)(lo >> 24),
+                        (float)(hi & 0xFFu), (float)((hi >> 8) & 0xFFu), (float)((hi >> 16) & 0xFFu), (float)(hi >> 24)};
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      float sc, mn;
+      if constexpr (TRANS) {
+        sc = as_f(r.s[i >> 1][(i & 1) * 2]);
+        mn = as_f(r.s[i >> 1][(i & 1) * 2 + 1]);
+      } else {
+        sc = as_f(r.s[0][0]);
+        mn = as_f(r.s[0][1]);
+      }
+      f[i] = __builtin_fmaf(sc, v[i], -mn);
+    }
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] = pk(f[2 * i], f[2 * i + 1]);
+    *reinterpret_cast<u32x4*>(bf + sw(g * 8 + (l >> 3), l & 7)) = o;
+  }
+  __device__ __forceinline__ void decode(const uint8_t* st, uint8_t* bf, int p) const {
+    Raw r[UPT];
+#pragma unroll
+    for (int j = 0; j < UPT; j++) r[j] = read(st, j, p);
+#pragma unroll
+    for (int j = 0; j < UPT; j++) write(r[j], bf, j, p);
+  }
+};
+
+template <int BM, int BN, int WGM, int NWM, int NWD, int NWL, bool TRANS, bool C_BF16, int ST, int TAG, bool FULL, bool GEN,
+          bool Q4>
 __global__ __launch_bounds__(64 * (NWM + NWD + NWL), 1) void gemm_q8f_kernel(Args g) {
   using S = Shape<BM, BN, WGM, NWM>;  // the MFMA waves' layout (epilogue included)
   constexpr int MB = S::MB, NB = S::NB, NT = 64 * (NWM + NWD + NWL);
   constexpr int LW = NWL ? NWL : NWM;  // NWL = 0: the MFMA waves issue the copies
   using LA = ProdA<BM, LW>;
-  using LB = FragQ8<BN, LW, NWD, TRANS>;
+  using LB = typename std::conditional<Q4, FragQ4<BN, LW, NWD, TRANS>, FragQ8<BN, LW, NWD, TRANS>>::type;
   static_assert(ST >= 3, "the loaders run two tiles ahead of the MFMA waves");
   constexpr int RAW = BM * 128 + LB::STAGE;
   constexpr int LDS = ST * RAW + 2 * BN * 128;
@@ -326,26 +427,26 @@ __global__ __launch_bounds__(64 * (NWM + NWD + NWL), 1) void gemm_q8f_kernel(Arg
   if (role == 0) gemm_epilogue<S, C_BF16, FULL>(g, acc, m0, n0, split);
 }
 
-template <int BM, int BN, int WGM, int NWM, int NWD, int NWL, bool TRANS, int ST, int TAG>
+template <int BM, int BN, int WGM, int NWM, int NWD, int NWL, bool TRANS, int ST, int TAG, bool Q4>
 static void launch_q8f_t(const Args& a, int c_bf16, int splits, hipStream_t s) {
   const dim3 grid(a.tiles_m * a.tiles_n, splits), block(64 * (NWM + NWD + NWL));
   const bool full = a.M % BM == 0 && a.N % BN == 0;
   const bool cb = c_bf16 && !a.partial;
   if (a.K2 > 0 && !a.ext_vec) {  // element-wise extension staging, general epilogue
-    if (cb) launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, true, ST, TAG, false, true>, grid, block, s, a);
-    else launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, false, ST, TAG, false, true>, grid, block, s, a);
+    if (cb) launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, true, ST, TAG, false, true, Q4>, grid, block, s, a);
+    else launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, false, ST, TAG, false, true, Q4>, grid, block, s, a);
   } else if (full) {
-    if (cb) launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, true, ST, TAG, true, false>, grid, block, s, a);
-    else launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, false, ST, TAG, true, false>, grid, block, s, a);
+    if (cb) launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, true, ST, TAG, true, false, Q4>, grid, block, s, a);
+    else launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, false, ST, TAG, true, false, Q4>, grid, block, s, a);
   } else {
-    if (cb) launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, true, ST, TAG, false, false>, grid, block, s, a);
-    else launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, false, ST, TAG, false, false>, grid, block, s, a);
+    if (cb) launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, true, ST, TAG, false, false, Q4>, grid, block, s, a);
+    else launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, false, ST, TAG, false, false, Q4>, grid, block, s, a);
   }
 }
-template <int BM, int BN, int WGM, int NWM, int NWD, int NWL, bool TRANS, int ST>
+template <int BM, int BN, int WGM, int NWM, int NWD, int NWL, bool TRANS, int ST, bool Q4>
 static void launch_q8f(const Args& a, int c_bf16, int splits, bool dx, hipStream_t s) {
-  if (dx) launch_q8f_t<BM, BN, WGM, NWM, NWD, NWL, TRANS, ST, 1>(a, c_bf16, splits, s);
-  else launch_q8f_t<BM, BN, WGM, NWM, NWD, NWL, TRANS, ST, 0>(a, c_bf16, splits, s);
+  if (dx) launch_q8f_t<BM, BN, WGM, NWM, NWD, NWL, TRANS, ST, 1, Q4>(a, c_bf16, splits, s);
+  else launch_q8f_t<BM, BN, WGM, NWM, NWD, NWL, TRANS, ST, 0, Q4>(a, c_bf16, splits, s);
 }
 
 // One shape: 128x128 output tiles, 4 MFMA waves of 64x64 (2x2), 4 decoder waves (one per SIMD),
@@ -353,11 +454,14 @@ static void launch_q8f(const Args& a, int c_bf16, int splits, bool dx, hipStream
 // tiles would halve the decode work per MFMA but need more than the 168 registers per lane that
 // a workgroup of 10 waves leaves (measured: the 8-MFMA-wave 256x128 form spills).
 bool dispatch_q8f(int tile, const Args& a, int bmode, int c_bf16, int sp, bool dx, hipStream_t s) {
-  if (bmode != SRC_Q8F && bmode != SRC_Q8FT) return false;
   if (tile != T128x128) return false;
-  if (bmode == SRC_Q8FT) launch_q8f<128, 128, 2, 4, 4, 2, true, 4>(a, c_bf16, sp, dx, s);
-  else launch_q8f<128, 128, 2, 4, 4, 2, false, 4>(a, c_bf16, sp, dx, s);
-  return true;
+  switch (bmode) {
+    case SRC_Q8FT: launch_q8f<128, 128, 2, 4, 4, 2, true, 4, false>(a, c_bf16, sp, dx, s); return true;
+    case SRC_Q8F: launch_q8f<128, 128, 2, 4, 4, 2, false, 4, false>(a, c_bf16, sp, dx, s); return true;
+    case SRC_Q4FT: launch_q8f<128, 128, 2, 4, 4, 2, true, 4, true>(a, c_bf16, sp, dx, s); return true;
+    case SRC_Q4F: launch_q8f<128, 128, 2, 4, 4, 2, false, 4, true>(a, c_bf16, sp, dx, s); return true;
+    default: return false;
+  }
 }
 
 }  // namespace g3

@@ -86,9 +86,10 @@ size_t planes_bytes(int qtype, int64_t n, size_t* qs_bytes);
 int repack_planes(int qtype, const void* raw, int64_t n, void* dst, QuantPlanes* out, hipStream_t s);
 int dequant_rows(const QuantPlanes& q, const int32_t* ids, float* out, int T, int D, hipStream_t s);
 int make_col_planes(const QuantPlanes& q, int rows, int cols, void* dst, QuantPlanes* out, hipStream_t s);
-// fragment planes (SRC_Q8F for trans = 0: B = W; SRC_Q8FT for trans = 1: B = W^T) of Q8_0 row
-// planes of W[rows][cols] into dst (frag_planes_bytes(rows*cols) bytes, 256-byte aligned)
-size_t frag_planes_bytes(int64_t n);
+// fragment planes (SRC_Q8F / SRC_Q4F for trans = 0: B = W; SRC_Q8FT / SRC_Q4FT for trans = 1:
+// B = W^T) of Q8_0 or Q4_K row planes of W[rows][cols] into dst (frag_planes_bytes(rows*cols,
+// qtype) bytes, 256-byte aligned)
+size_t frag_planes_bytes(int64_t n, int qtype);
 int make_frag_planes(const QuantPlanes& q, int rows, int cols, int trans, void* dst, Operand* out, hipStream_t s);
 // one launch decoding many matrices; `first` = index of the job's first 64x64 tile in the grid
 struct DequantJob {

@@ -232,21 +232,63 @@ __global__ void frag_planes_q8_kernel(const int8_t* __restrict__ qs, const float
     scales[y] = __builtin_bit_cast(uint16_t, (_Float16)v);
   }
 }
-size_t frag_planes_bytes(int64_t n) { return (size_t)n + (size_t)n / 16; }
+__global__ void frag_planes_q4k_kernel(const uint8_t* __restrict__ qs, const float* __restrict__ sm, int rows,
+                                       int cols, int trans, uint8_t* __restrict__ codes, float* __restrict__ pairs) {
+  const int N = trans ? cols : rows, K = trans ? rows : cols;
+  const int64_t words = (int64_t)N * K / 8, npair = (int64_t)N * K / 32;
+  const int kts = K / 64;
+  for (int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; x < words; x += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t blk = x >> 8;  // 256 four-byte words per 32 x 64 block
+    const int g = (int)(x & 255);
+    const int64_t rb = blk / kts;
+    const int kt = (int)(blk - rb * kts);
+    const int64_t r = rb * 32 + (g >> 3);
+    const int64_t k0 = (int64_t)kt * 64 + (g & 7) * 8;
+    uint32_t w = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int64_t e = trans ? (k0 + i) * cols + r : r * cols + k0 + i;
+      w |= q4k_code(qs, e) << (i < 4 ? 8 * i : 8 * (i - 4) + 4);
+    }
+    reinterpret_cast<uint32_t*>(codes)[x] = w;
+  }
+  for (int64_t y = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; y < npair; y += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t rb = y / K;
+    const int rem = (int)(y - rb * K);
+    int64_t src;
+    if (trans) {
+      src = ((int64_t)rem * cols + rb * 32) / 32;
+    } else {
+      const int kt = rem >> 6, j = (rem >> 5) & 1, rl = rem & 31;
+      src = ((rb * 32 + rl) * cols + kt * 64 + j * 32) / 32;
+    }
+    pairs[2 * y] = sm[2 * src];
+    pairs[2 * y + 1] = sm[2 * src + 1];
+  }
+}
+size_t frag_planes_bytes(int64_t n, int qtype) {
+  return qtype == SMHIP_QTYPE_Q4_K ? (size_t)n / 2 + (size_t)n / 4 : (size_t)n + (size_t)n / 16;
+}
 int make_frag_planes(const QuantPlanes& q, int rows, int cols, int trans, void* dst, Operand* out, hipStream_t s) {
-  SMHIP_REQUIRE(q.kind == SMHIP_QTYPE_Q8_0, "fragment planes: Q8_0 only");
+  SMHIP_REQUIRE(q.kind == SMHIP_QTYPE_Q8_0 || q.kind == SMHIP_QTYPE_Q4_K, "fragment planes: Q8_0 or Q4_K");
   SMHIP_REQUIRE(q.n == (int64_t)rows * cols, "fragment planes: shape does not match the planes");
   const int N = trans ? cols : rows, K = trans ? rows : cols;
   SMHIP_REQUIRE(N % 32 == 0 && K % 64 == 0, "fragment planes: B rows must be a multiple of 32 and K of 64");
   SMHIP_REQUIRE(((uintptr_t)dst & 255) == 0, "fragment planes: destination must be 256-byte aligned");
-  out->mode = trans ? SRC_Q8FT : SRC_Q8F;
+  const bool q8 = q.kind == SMHIP_QTYPE_Q8_0;
+  const size_t cb = q8 ? (size_t)q.n : (size_t)q.n / 2;  // code bytes
+  out->mode = q8 ? (trans ? SRC_Q8FT : SRC_Q8F) : (trans ? SRC_Q4FT : SRC_Q4F);
   out->p = dst;
-  out->s = (const float*)((char*)dst + q.n);  // fp16 scales (see SrcMode)
+  out->s = (const float*)((char*)dst + cb);  // fp16 scales (Q8_0) or fp32 pairs (Q4_K), see SrcMode
   out->ld = K;
-  const int64_t groups = q.n / 8;
-  const int g = (int)std::min<int64_t>((groups + 255) / 256, (int64_t)num_cus() * 16);
-  hipLaunchKernelGGL(frag_planes_q8_kernel, dim3(g), dim3(256), 0, s, (const int8_t*)q.qs, q.sc, rows, cols, trans,
-                     (uint8_t*)dst, (uint16_t*)((char*)dst + q.n));
+  const int64_t work = q.n / 8;
+  const int g = (int)std::min<int64_t>((work + 255) / 256, (int64_t)num_cus() * 16);
+  if (q8)
+    hipLaunchKernelGGL(frag_planes_q8_kernel, dim3(g), dim3(256), 0, s, (const int8_t*)q.qs, q.sc, rows, cols, trans,
+                       (uint8_t*)dst, (uint16_t*)((char*)dst + cb));
+  else
+    hipLaunchKernelGGL(frag_planes_q4k_kernel, dim3(g), dim3(256), 0, s, (const uint8_t*)q.qs, q.sc, rows, cols,
+                       trans, (uint8_t*)dst, (float*)((char*)dst + cb));
   SMHIP_CHECK_LAUNCH();
   return SMHIP_OK;
 }
