@@ -230,13 +230,17 @@ def main():
     tf = lambda fl, ms: round(fl / (ms * 1e-3) / 1e12, 2) if ms else None
     if dx_n:  # dominant kernel: the backward dX GEMMs through the frozen quantised base
         k_ms, k_n, k_fl = dx_ms, dx_n, dx_fl
-        if os.environ.get("SMHIP_BASE_WS") == "1" or cfg.base_qtype != QTYPE_Q8_0:
+        if os.environ.get("SMHIP_BASE_WS") == "1":
             kname = ("gemm_kernel<..., TAG 1>: backward dX = dY W through the frozen base (bf16 copy decoded "
                      "each step), bf16 MFMA")
-        else:
+        elif cfg.base_qtype == QTYPE_Q8_0:
             kname = ("gemm_q8f_kernel<128, 128, 2, 4, 4, 2, true, ..., TAG 1, ...>: backward dX = dY W through "
                      "the frozen Q8_0 base, int8 codes and fp16 scales copied to LDS and decoded there "
                      "(never expanded in HBM), bf16 MFMA")
+        else:
+            kname = ("gemm_q8f_kernel<128, 128, 2, 4, 4, 2, true, ..., TAG 1, ..., Q4 true>: backward dX = dY W "
+                     "through the frozen Q4_K base, 4-bit codes and fp32 scale/min pairs copied to LDS and "
+                     "decoded there (never expanded in HBM), bf16 MFMA")
     else:
         k_ms, k_n, k_fl = all_ms, all_n, all_fl
         kname = "gemm_kernel (all linears, fwd+bwd)"
