@@ -51,68 +51,30 @@ __device__ inline bf16x8 pack8(const floatx16& a, int e0) {
   u.w = pack_bf2(a[e0 + 6], a[e0 + 7]);
   return as_bf16x8(u);
 }
-// Transposed [D][NR] LDS tiles.  With SW, for D = 128 and NR = 64, the rows are unpadded and
-// each row's 4-element column chunks are XOR-swizzled by tswz(d): the staging stores (16 lanes
-// per source row, 8 consecutive d each) and the 8-byte operand reads below are then both free
-// of bank conflicts (measured; with the padded layout, pitch NR + 4, the stores of lanes d and
-// d + 8 share banks).  Only the dQ kernel uses it: the swizzle costs address registers, which
-// pushes the dK/dV kernel (already at 256) into spills, and in the forward kernel the extra
-// address arithmetic outweighed the conflicts removed (measured 42.5 -> 44 us at 4x1024).
-template <int D, int NR, bool SW>
-struct TLay {
-  static constexpr bool SWZ = SW && D == 128 && NR == 64;
-  static constexpr int TP = SWZ ? NR : NR + 4;  // row pitch in elements
-};
-// chunk swizzle of transposed row d: (d / 8) ^ 2 (d % 8), 4 bits.  An XOR (not a sum) so that
-// for d = 32 i + l it splits into a constant part 4 i and a lane part.
-__device__ inline int tswz(int d) { return ((d >> 3) ^ (2 * (d & 7))) & 15; }
-// operand from transposed tile row d = 32 i + lane % 32: keys c16 + half*4 + {0..3} and
-// c16 + 8 + half*4 + {0..3} (c16 a multiple of 16, half = lane / 32)
-template <int D, int NR, bool SW>
+// operand from a transposed LDS tile [D][NR + 4]: row d = 32 i + lane % 32, keys
+// c16 + half*4 + {0..3} and c16 + 8 + half*4 + {0..3} (half = lane / 32)
+template <int NR>
 __device__ inline bf16x8 tload(const uint16_t* tile, int i, int c16, int lane) {
-  const int l = lane & 31;
-  const uint16_t* row = tile + (i * 32 + l) * TLay<D, NR, SW>::TP;
-  const uint16_t *p0, *p1;
-  if constexpr (TLay<D, NR, SW>::SWZ) {
-    int x = (lane >> 5) ^ tswz(l);  // lane part of the chunk index
-    // opaque copy: the chunk addresses are formed at each read rather than all eight kept live
-    // across the query loop (they would push the dK/dV kernel into spills)
-    asm volatile("" : "+v"(x));
-    const int kc = ((c16 >> 2) ^ (4 * i)) & 15;  // constant part (bit 1 clear)
-    p0 = row + 4 * (kc ^ x);
-    p1 = row + 4 * ((kc ^ 2) ^ x);
-  } else {
-    const int k = c16 + (lane >> 5) * 4;
-    p0 = row + k;
-    p1 = row + k + 8;
-  }
-  uint2 lo = *reinterpret_cast<const uint2*>(p0);
-  uint2 hi = *reinterpret_cast<const uint2*>(p1);
+  const uint16_t* p = tile + (i * 32 + (lane & 31)) * (NR + 4) + c16 + (lane >> 5) * 4;
+  uint2 lo = *reinterpret_cast<const uint2*>(p);
+  uint2 hi = *reinterpret_cast<const uint2*>(p + 8);
   return as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
 }
 
 // Register-prefetched staging: load() issues the global reads of a [NR][D] row tile (pairs
 // of rows per 16-byte column chunk) into registers, store() writes them to LDS as [NR][D+8]
-// and/or transposed [D][NR+8].  Loading tile t+1 before the MFMAs of tile t hides the
+// and/or transposed [D][NR+4].  Loading tile t+1 before the MFMAs of tile t hides the
 // global latency behind the compute.
-template <int D, int NR, int NT = 256, bool SW = false>
+template <int D, int NR, int NT = 256>
 struct Pref {
   static constexpr int U = (NR / 2) * (D / 8);  // (row pair, chunk) units
   static constexpr int PER = (U + NT - 1) / NT;
   static_assert(PER <= 2, "Pref holds at most two units per thread");
   uint4 a0, b0, a1, b1;  // named registers: no dynamically indexed (scratch) arrays
-  // unit c = (row pair rp, 8-column chunk dc).  Swizzled layout: 16 consecutive units are one
-  // row pair's 16 chunks (whole 256-byte rows loaded and stored); padded layout: consecutive
-  // units walk the row pairs of one chunk.
-  static constexpr bool SWZ = TLay<D, NR, SW>::SWZ;
+  // unit c = (row pair rp, 8-column chunk dc): consecutive units walk the row pairs of a chunk
   __device__ static inline void unit(int c, int& rp, int& dc) {
-    if constexpr (SWZ) {
-      rp = c / (D / 8);
-      dc = (c % (D / 8)) * 8;
-    } else {
-      rp = c % (NR / 2);
-      dc = (c / (NR / 2)) * 8;
-    }
+    rp = c % (NR / 2);
+    dc = (c / (NR / 2)) * 8;
   }
   // unit c's two rows; units past U (only when U is not a multiple of NT) read row pair 0
   __device__ static inline uint4 ld1(const uint16_t* __restrict__ g, int64_t ld, int r0, int c, int odd) {
@@ -131,7 +93,7 @@ struct Pref {
   }
   template <bool ROWS, bool TRANS>
   __device__ inline void store1(uint16_t* sRow, uint16_t* sT, int c, const uint4& a, const uint4& b) const {
-    constexpr int RP = D + 8, TP = TLay<D, NR, SW>::TP;
+    constexpr int RP = D + 8, TP = NR + 4;
     if (c >= U) return;
     int rp, dc;
     unit(c, rp, dc);
@@ -145,9 +107,7 @@ struct Pref {
       for (int j = 0; j < 8; j++) {
         const uint32_t lo = (j & 1) ? (av[j >> 1] >> 16) : (av[j >> 1] & 0xFFFFu);
         const uint32_t hi = (j & 1) ? (bv[j >> 1] >> 16) : (bv[j >> 1] & 0xFFFFu);
-        const int d = dc + j;
-        const int col = SWZ ? 4 * ((rp >> 1) ^ tswz(d)) + 2 * (rp & 1) : 2 * rp;
-        *reinterpret_cast<uint32_t*>(sT + d * TP + col) = lo | (hi << 16);
+        *reinterpret_cast<uint32_t*>(sT + (dc + j) * TP + 2 * rp) = lo | (hi << 16);
       }
     }
   }
@@ -247,7 +207,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_fwd_kernel(const uint16_t
                                                      const uint16_t* __restrict__ v, uint16_t* __restrict__ o,
                                                      float* __restrict__ lse, int S, int Hq, int Hkv, int64_t ldq,
                                                      int64_t ldk, int64_t ldv, int64_t ldo, float sl2) {
-  constexpr int KB = 64, KP = D + 8, VP = TLay<D, KB, false>::TP, NT = PAIR ? 512 : 256;
+  constexpr int KB = 64, KP = D + 8, VP = KB + 4, NT = PAIR ? 512 : 256;
   __shared__ __attribute__((aligned(16))) uint16_t sK[KB * KP];
   __shared__ __attribute__((aligned(16))) uint16_t sVt[D * VP];
   const int nb = PAIR ? 2 * (int)gridDim.x : (int)gridDim.x;
@@ -332,7 +292,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_fwd_kernel(const uint16_t
       const bf16x8 pf = pack8(sacc[c >> 1], 8 * (c & 1));
 #pragma unroll
       for (int i = 0; i < D / 32; i++) {
-        const bf16x8 vf = tload<D, KB, false>(sVt, i, c * 16, lane);
+        const bf16x8 vf = tload<KB>(sVt, i, c * 16, lane);
         oacc[i] = mfma16(vf, pf, oacc[i]);
       }
     }
@@ -526,7 +486,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_bwd_dkdv_kernel(
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
     TG* __restrict__ dKh, TG* __restrict__ dVh, int S, int Hq, int Hkv, int64_t ldq, int64_t ldk,
     int64_t ldv, int64_t lddo, float sl2, float scale) {
-  constexpr int QB = 64, NQ = QB / 32, RP = D + 8, TP = TLay<D, QB, false>::TP, NT = PAIR ? 512 : 256;
+  constexpr int QB = 64, NQ = QB / 32, RP = D + 8, TP = QB + 4, NT = PAIR ? 512 : 256;
   __shared__ __attribute__((aligned(16))) uint16_t sQ[QB * RP];
   __shared__ __attribute__((aligned(16))) uint16_t sQt[D * TP];
   __shared__ __attribute__((aligned(16))) uint16_t sdO[QB * RP];
@@ -621,8 +581,8 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_bwd_dkdv_kernel(
         const bf16x8 sf = pack8(dpacc, 8 * c);
 #pragma unroll
         for (int i = 0; i < D / 32; i++) {
-          dv[i] = mfma16(pf, tload<D, QB, false>(sdOt, i, jb * 32 + c * 16, lane), dv[i]);
-          dk[i] = mfma16(sf, tload<D, QB, false>(sQt, i, jb * 32 + c * 16, lane), dk[i]);
+          dv[i] = mfma16(pf, tload<QB>(sdOt, i, jb * 32 + c * 16, lane), dv[i]);
+          dk[i] = mfma16(sf, tload<QB>(sQt, i, jb * 32 + c * 16, lane), dk[i]);
         }
         __builtin_amdgcn_sched_barrier(0);  // bounds the transposed fragments in flight
       }
@@ -773,7 +733,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_bwd_dq_kernel(
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
     TG* __restrict__ dq, int S, int Hq, int Hkv, int64_t ldq, int64_t ldk, int64_t ldv, int64_t lddo,
     int64_t lddq, float sl2, float scale) {
-  constexpr int KB = 64, RP = D + 8, TP = TLay<D, KB, true>::TP, NT = PAIR ? 512 : 256;
+  constexpr int KB = 64, RP = D + 8, TP = KB + 4, NT = PAIR ? 512 : 256;
   __shared__ __attribute__((aligned(16))) uint16_t sK[KB * RP];
   __shared__ __attribute__((aligned(16))) uint16_t sKt[D * TP];
   __shared__ __attribute__((aligned(16))) uint16_t sV[KB * RP];
@@ -802,7 +762,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_bwd_dq_kernel(
   const uint16_t* vb = v + (int64_t)b * S * ldv + kvh * D;
   const int kend = (nb - (int)blockIdx.x) * 128;  // the longer block of the workgroup
   const int wq_last = qb * 128 + w * 32 + 31;
-  Pref<D, KB, NT, true> pk, pv;
+  Pref<D, KB, NT> pk, pv;
   pk.load(kb, ldk, 0);
   pv.load(vb, ldv, 0);
   for (int k0 = 0; k0 < kend; k0 += KB) {
@@ -842,7 +802,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_bwd_dq_kernel(
     for (int c = 0; c < 4; c++) {
       const bf16x8 sf = pack8(s[c >> 1], 8 * (c & 1));
 #pragma unroll
-      for (int i = 0; i < D / 32; i++) acc[i] = mfma16(tload<D, KB, true>(sKt, i, c * 16, lane), sf, acc[i]);
+      for (int i = 0; i < D / 32; i++) acc[i] = mfma16(tload<KB>(sKt, i, c * 16, lane), sf, acc[i]);
     }
   }
   TG* qrow = dq + ((int64_t)b * S + qi) * lddq + h * D;

@@ -86,3 +86,43 @@ def test_flash_forward_backward(orc, dev, B, S, Hq, Hkv, D):
                                            D, qd, kvd, kvd, qd, qd, qd, kvd, kvd, s))
     torch.cuda.synchronize()
     assert torch.equal(dq, dq2)
+
+
+def _run(L, dev, q, k, v, dO, B, S, Hq, Hkv, D, shift):
+    """Forward + backward with q and k starting `shift` elements into their buffers."""
+    s = torch.cuda.current_stream().cuda_stream
+    qd, kvd = Hq * D, Hkv * D
+
+    def place(a, off):
+        buf = torch.zeros(a.size + 8, device=dev, dtype=torch.bfloat16)
+        buf[off:off + a.size] = torch.from_numpy(a.ravel()).to(dev).to(torch.bfloat16)
+        return buf, buf[off:].data_ptr()
+
+    (bq, pq), (bk, pk) = place(q, shift), place(k, shift)
+    (bv, pv), (bo, pdo) = place(v, 0), place(dO, 0)
+    o = torch.zeros(B * S, qd, device=dev, dtype=torch.bfloat16)
+    lse = torch.empty(B, Hq, S, device=dev)
+    check(L.smhip_flash_attention_forward(pq, pk, pv, o.data_ptr(), lse.data_ptr(), B, S, Hq, Hkv, D, qd, kvd, kvd, qd, s))
+    dq = torch.empty(B * S, qd, device=dev)
+    dk = torch.empty(B * S, kvd, device=dev)
+    dv = torch.empty(B * S, kvd, device=dev)
+    check(L.smhip_flash_attention_backward(pq, pk, pv, o.data_ptr(), pdo, lse.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                                           dv.data_ptr(), B, S, Hq, Hkv, D, qd, kvd, kvd, qd, qd, qd, kvd, kvd, s))
+    torch.cuda.synchronize()
+    return o, lse, dq, dk, dv
+
+
+@pytest.mark.parametrize("S", [256, 384])
+def test_flash_d128_dma_matches_register_staging(dev, S):
+    """Head dim 128 with 16-byte aligned q/k/v/dO takes the DMA-staged kernels (tiles copied global
+    -> LDS, transposed operands read with ds_read_b64_tr_b16); q and k 8 bytes off that alignment
+    take the register-staged kernels.  Both compute in the same order: bit-identical."""
+    B, Hq, Hkv, D = 2, 4, 2, 128
+    rng = np.random.default_rng(S)
+    q, dO = (_bf16_round(rng.standard_normal((B, S, Hq, D)).astype(np.float32)) for _ in range(2))
+    k, v = (_bf16_round(rng.standard_normal((B, S, Hkv, D)).astype(np.float32)) for _ in range(2))
+    L = sharpmind_amd.lib()
+    a = _run(L, dev, q, k, v, dO, B, S, Hq, Hkv, D, 0)
+    b = _run(L, dev, q, k, v, dO, B, S, Hq, Hkv, D, 4)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
