@@ -379,6 +379,139 @@ __global__ __launch_bounds__(256) void skinny_reduce_batch_kernel(BatchArgs b) {
   }
 }
 
+// ---------------------------------------------------------------- row-block form, no split
+// For k-contiguous Big and K % 128 == 0: a workgroup owns 16 rows of C and its NW waves (8, or 4
+// when K % 256 != 0) take an equal share of K each, loading v_mfma_f32_16x16x32_bf16 fragments straight from memory into
+// registers (Big once from HBM, two 4-slice batches in flight per wave; Small from L2).  The
+// NW 16 x n partial blocks are added in wave order through LDS and written by wave 0: one
+// launch, no partial planes, a fixed summation order.  Small is read k-contiguous from memory
+// (SMALLK) or, when it is [K][n] row-major, staged whole into LDS (K n 2 <= RS_SMALL bytes) and
+// read with ds_read_b64_tr_b16, which hands each lane four k-rows of its column.
+constexpr int RS_SMALL = 96 * 1024;
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_s4;
+
+template <int NB, bool SMALLK>
+__device__ __forceinline__ bf16x8 rows_small_frag(const Args& a, const uint8_t* sm, int j, int k0, int lane) {
+  const int c = 16 * j + (lane & 15), g = lane >> 4;
+  if constexpr (SMALLK) {
+    return *reinterpret_cast<const bf16x8*>((const uint16_t*)a.small + (int64_t)c * a.lds + k0 + 8 * g);
+  } else {
+    // tr read over 16 lanes: source lane s reads 4 columns 16 j + 4 (s % 4) of k-row s / 4;
+    // destination lane s gets column 16 j + s of the 4 rows
+    const int s = lane & 15;
+    const uint8_t* p = sm + ((int64_t)(k0 + 8 * g + (s >> 2)) * a.n + 16 * j + 4 * (s & 3)) * 2;
+    short4v lo, hi;
+#if defined(__HIP_DEVICE_COMPILE__)
+    lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)p);
+    hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p + 4 * a.n * 2));
+#else
+    lo = hi = short4v{};
+#endif
+    const uint2 x = __builtin_bit_cast(uint2, lo), y = __builtin_bit_cast(uint2, hi);
+    return __builtin_bit_cast(bf16x8, make_uint4(x.x, x.y, y.x, y.y));
+  }
+}
+
+template <int NB, bool SMALLK, bool TRANS_OUT, bool C_BF16, int NW>
+__global__ __launch_bounds__(64 * NW) void skinny_rows_kernel(Args a) {
+  constexpr int P = 4;  // 32-k slices per batch
+  constexpr int RED = NW * NB * 64 * 16;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[(SMALLK ? 0 : RS_SMALL) + RED];
+  uint8_t* red = smem + (SMALLK ? 0 : RS_SMALL);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int m0 = blockIdx.x * 16;
+  if constexpr (!SMALLK) {  // stage Small [K][n] (contiguous, K n 2 bytes)
+    const int nv = a.K * a.n / 8;
+    for (int i = threadIdx.x; i < nv; i += 64 * NW)
+      reinterpret_cast<uint4*>(smem)[i] = reinterpret_cast<const uint4*>(a.small)[i];
+    __syncthreads();
+  }
+  const int row = min(m0 + (lane & 15), a.M - 1);
+  const uint16_t* brow = (const uint16_t*)a.big + (int64_t)row * a.ldb + 8 * (lane >> 4);
+  const int kq = a.K / NW, kb = w * kq, nsl = kq / 32;
+  floatx4 acc[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  bf16x8 b0[P], b1[P], s0[P][SMALLK ? NB : 1], s1[P][SMALLK ? NB : 1];
+  auto load = [&](bf16x8(&bb)[P], bf16x8(&ss)[P][SMALLK ? NB : 1], int sl0) {
+#pragma unroll
+    for (int t = 0; t < P; t++) {
+      const int sl = min(sl0 + t, nsl - 1);
+      bb[t] = *reinterpret_cast<const bf16x8*>(brow + kb + 32 * sl);
+      if constexpr (SMALLK) {
+#pragma unroll
+        for (int j = 0; j < NB; j++) ss[t][j] = rows_small_frag<NB, true>(a, nullptr, j, kb + 32 * sl, lane);
+      }
+    }
+  };
+  auto compute = [&](bf16x8(&bb)[P], bf16x8(&ss)[P][SMALLK ? NB : 1], int sl0) {
+#pragma unroll
+    for (int t = 0; t < P; t++) {
+      if (sl0 + t >= nsl) break;
+#pragma unroll
+      for (int j = 0; j < NB; j++) {
+        const bf16x8 f = SMALLK ? ss[t][SMALLK ? j : 0] : rows_small_frag<NB, false>(a, smem, j, kb + 32 * (sl0 + t), lane);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bb[t], f, acc[j], 0, 0, 0);
+      }
+    }
+  };
+  load(b0, s0, 0);
+  for (int sl = 0; sl < nsl; sl += 2 * P) {
+    if (sl + P < nsl) load(b1, s1, sl + P);
+    compute(b0, s0, sl);
+    if (sl + 2 * P < nsl) load(b0, s0, sl + 2 * P);
+    if (sl + P < nsl) compute(b1, s1, sl + P);
+  }
+  // wave partials -> LDS, summed in wave order by wave 0
+#pragma unroll
+  for (int j = 0; j < NB; j++) *reinterpret_cast<floatx4*>(red + ((w * NB + j) * 64 + lane) * 16) = acc[j];
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    floatx4 v = *reinterpret_cast<const floatx4*>(red + (j * 64 + lane) * 16);
+#pragma unroll
+    for (int q = 1; q < NW; q++) v += *reinterpret_cast<const floatx4*>(red + ((q * NB + j) * 64 + lane) * 16);
+    const int col = 16 * j + (lane & 15);
+    if (col >= a.n) continue;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int r = m0 + 4 * (lane >> 4) + e;
+      if (r >= a.M || !mask_keep(a.mask, col, r, a.M)) continue;
+      const int64_t ci = TRANS_OUT ? (int64_t)col * a.ldc + r : (int64_t)r * a.ldc + col;
+      float o = a.alpha * v[e];
+      if constexpr (C_BF16) {
+        uint16_t* c = (uint16_t*)a.C + ci;
+        if (a.beta != 0.f) o += a.beta * bf2f(*c);
+        *c = f2bf(o);
+      } else {
+        float* c = (float*)a.C + ci;
+        if (a.beta != 0.f) o += a.beta * *c;
+        *c = o;
+      }
+    }
+  }
+}
+
+template <bool SMALLK, bool TRANS_OUT, bool C_BF16, int NW>
+static void launch_rows_nw(int nb, const Args& a, hipStream_t s) {
+  const dim3 grid(ceil_div(a.M, 16)), block(64 * NW);
+  switch (nb) {
+    case 1: hipLaunchKernelGGL((skinny_rows_kernel<1, SMALLK, TRANS_OUT, C_BF16, NW>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((skinny_rows_kernel<2, SMALLK, TRANS_OUT, C_BF16, NW>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((skinny_rows_kernel<3, SMALLK, TRANS_OUT, C_BF16, NW>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((skinny_rows_kernel<4, SMALLK, TRANS_OUT, C_BF16, NW>), grid, block, 0, s, a); break;
+  }
+}
+// eight waves (two per SIMD, twice the loads in flight) when K splits into eighths of whole
+// 32-k slices, else four
+template <bool SMALLK, bool TRANS_OUT, bool C_BF16>
+static void launch_rows(int nb, const Args& a, hipStream_t s) {
+  if (a.K % 256 == 0) launch_rows_nw<SMALLK, TRANS_OUT, C_BF16, 8>(nb, a, s);
+  else launch_rows_nw<SMALLK, TRANS_OUT, C_BF16, 4>(nb, a, s);
+}
+
 template <bool BIGK, bool SMALLK, int NB>
 static void launch(const Args& a, dim3 grid, bool trans, bool cbf, hipStream_t s) {
   if (trans) {
@@ -458,6 +591,22 @@ int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, c
   a.M = M; a.n = n; a.K = K;
   a.C = C; a.ldc = ldc; a.alpha = alpha; a.beta = beta;
   a.mask = mask;
+  // k-contiguous Big, K a multiple of 128 and K n <= 64Ki (Small at most 128 KiB): the row-block
+  // kernel, no split and no reduction pass.  Its workgroups re-read Small once per 16 rows, which
+  // for larger Small costs more than the split-K kernel's reduction pass (measured: 4096 x 48 x
+  // 1024 9.7 -> 6.8 us, 4096 x 16 x 3072 8.7 -> 7.5 us, but 4096 x 48 x 4096 14.5 -> 17.7 us).
+  if (big_k && K % 128 == 0 && (int64_t)K * n <= 65536 && (small_k || (int64_t)K * n * 2 <= RS_SMALL)) {
+    a.partial = nullptr;
+    const int ev0 = prof_mark(s);
+#define SMHIP_ROWS(SK)                                                           \
+  if (trans_out) { if (c_bf16) launch_rows<SK, true, true>(n / 16, a, s); else launch_rows<SK, true, false>(n / 16, a, s); } \
+  else { if (c_bf16) launch_rows<SK, false, true>(n / 16, a, s); else launch_rows<SK, false, false>(n / 16, a, s); }
+    if (small_k) { SMHIP_ROWS(true) } else { SMHIP_ROWS(false) }
+#undef SMHIP_ROWS
+    SMHIP_CHECK_LAUNCH();
+    prof_add(PROF_GEMM, ev0, prof_mark(s), 2.0 * M * n * (double)K, M, n, K);
+    return 1;
+  }
   const int mt = ceil_div(M, MT), nk = K / BKT;
   // splits: two workgroups per CU; fewer while the fp32 partials (written and read back)
   // exceed a quarter of the bytes of Big, as long as every CU keeps a workgroup

@@ -84,10 +84,15 @@ def test_qgemm_bf16(orc, dev, qtype, trans, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K,am,bm", [(6144, 32, 4096, 3, 3), (4096, 48, 4096, 2, 2), (1024, 16, 4096, 3, 3),
-                                         (48, 4096, 4096, 2, 2)])
+                                         (48, 4096, 4096, 2, 2), (4096, 48, 1024, 2, 3), (4100, 16, 3072, 2, 3),
+                                         (4096, 32, 6144, 2, 2), (2000, 64, 1152, 2, 2), (16, 1000, 640, 2, 2),
+                                         (4096, 16, 1024, 2, 2), (1000, 32, 1152, 2, 2)])
 def test_skinny_split_reduction_repeatable(dev, M, N, K, am, bm):
-    """Rank-sized products split K across workgroups and add the splits in a fixed order:
-    back-to-back calls on one stream give the same bits, and each matches float64."""
+    """Rank-sized products split K across workgroups (split-K partial planes, or the waves of a
+    row-block workgroup when the large operand is k-contiguous) and add the splits in a fixed
+    order: back-to-back calls on one stream give the same bits, and each matches float64.  The
+    row-block cases cover a k-contiguous small operand (read from memory) and a [K][n] one
+    (staged in LDS, read transposed), ragged M, and the rank-as-M form (output transposed)."""
     rng = np.random.default_rng(M + N)
     a = _rnd((M, K), rng)
     b = _rnd((N, K), rng)
