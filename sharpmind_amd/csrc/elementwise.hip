@@ -172,6 +172,57 @@ __global__ __launch_bounds__(256) void column_reduce_add_kernel(const float* __r
   }
 }
 
+// Same sum for D % 16 == 0 and 16-byte aligned rows: block of 256 = 4 float4 column lanes (16
+// columns) x 64 row groups; group j sums rows g = j, j+64, ... with eight float4 loads in flight,
+// so G <= 512 partial rows are one round trip; then the 64 group sums are added in ascending j.
+__global__ __launch_bounds__(256) void column_reduce_add_v4_kernel(const float* __restrict__ part,
+                                                                   float* __restrict__ dst, int G, int D) {
+  __shared__ float4 sh[64][4];
+  const int c = threadIdx.x & 3, j = threadIdx.x >> 2;
+  const int d = blockIdx.x * 16 + 4 * c;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int g0 = j; g0 < G; g0 += 64 * 8) {
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int g = g0 + 64 * u;
+      v[u] = g < G ? ld4(part + (int64_t)g * D + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      s.x += v[u].x;
+      s.y += v[u].y;
+      s.z += v[u].z;
+      s.w += v[u].w;
+    }
+  }
+  sh[j][c] = s;
+  __syncthreads();
+  if (j == 0) {
+    float4 t = sh[0][c];
+    for (int k = 1; k < 64; k++) {
+      const float4 q = sh[k][c];
+      t.x += q.x;
+      t.y += q.y;
+      t.z += q.z;
+      t.w += q.w;
+    }
+    float4 o = ld4(dst + d);
+    o.x += t.x;
+    o.y += t.y;
+    o.z += t.z;
+    o.w += t.w;
+    st4(dst + d, o);
+  }
+}
+
+static void column_reduce_add(const float* part, float* dst, int G, int D, hipStream_t s) {
+  if (D % 16 == 0 && (uintptr_t)part % 16 == 0 && (uintptr_t)dst % 16 == 0)
+    hipLaunchKernelGGL(column_reduce_add_v4_kernel, dim3(D / 16), dim3(256), 0, s, part, dst, G, D);
+  else
+    hipLaunchKernelGGL(column_reduce_add_kernel, dim3(ceil_div(D, 16)), dim3(256), 0, s, part, dst, G, D);
+}
+
 template <int VEC, int NCH, bool FROM_X, bool HAS_DW>
 static int rmsnorm_bwd_launch(const float* dY, const float* x, const float* rinv, const float* w,
                               float* dw, float* dX, int T, int D, int accumulate, uint16_t* dXb,
@@ -191,8 +242,7 @@ static int rmsnorm_bwd_launch(const float* dY, const float* x, const float* rinv
                      dY, x, rinv, w, dX, part, T, D, accumulate, dXb);
   SMHIP_CHECK_LAUNCH();
   if (HAS_DW) {
-    hipLaunchKernelGGL(column_reduce_add_kernel, dim3(ceil_div(D, 16)), dim3(256), 0, s, part, dw,
-                       G, D);
+    column_reduce_add(part, dw, G, D, s);
     SMHIP_CHECK_LAUNCH();
   }
   return SMHIP_OK;
@@ -368,8 +418,8 @@ int layernorm_backward(const float* dY, const float* x, const float* w, float* d
   hipLaunchKernelGGL(layernorm_bwd_kernel, dim3(G), dim3(kBlock), 8 * D * sizeof(float), s, dY, x,
                      w, dX, part, part + (size_t)G * D, T, D, eps);
   SMHIP_CHECK_LAUNCH();
-  if (dw) hipLaunchKernelGGL(column_reduce_add_kernel, dim3(ceil_div(D, 16)), dim3(256), 0, s, part, dw, G, D);
-  if (db) hipLaunchKernelGGL(column_reduce_add_kernel, dim3(ceil_div(D, 16)), dim3(256), 0, s, part + (size_t)G * D, db, G, D);
+  if (dw) column_reduce_add(part, dw, G, D, s);
+  if (db) column_reduce_add(part + (size_t)G * D, db, G, D, s);
   SMHIP_CHECK_LAUNCH();
   return SMHIP_OK;
 }
@@ -584,18 +634,21 @@ int rope_apply(float* x, const float* cosT, const float* sinT, int B, int S, int
 // Cross-entropy + softmax gradient (Gradients.cs:33-84), loss (CrossEntropyLoss.cs:44-104)
 // ============================================================================
 // labelled-row count and (below) mean loss: one 1024-thread block, fixed-order tree reductions
-__global__ __launch_bounds__(1024) void count_labels_kernel(const int32_t* __restrict__ labels, int T, int ignoreId,
-                                                            int* __restrict__ count) {
-  __shared__ int sh[1024];
+// Non-ignored labels of the batch, counted by every workgroup itself (T int reads from L2, one
+// round for T <= 8 NT) instead of a separate single-block launch; block 0 also stores it for
+// the mean-loss kernel.  Integer sums: exact in any order.
+template <int NT>
+__device__ inline int block_count_labels(const int32_t* __restrict__ labels, int T, int ignoreId, int* __restrict__ count) {
+  __shared__ int shc[NT / 64];
   int c = 0;
-  for (int t = threadIdx.x; t < T; t += 1024) c += labels[t] != ignoreId;
-  sh[threadIdx.x] = c;
+  for (int t = threadIdx.x; t < T; t += NT) c += labels[t] != ignoreId;
+  for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+  if ((threadIdx.x & 63) == 0) shc[threadIdx.x >> 6] = c;
   __syncthreads();
-  for (int o = 512; o > 0; o >>= 1) {
-    if ((int)threadIdx.x < o) sh[threadIdx.x] += sh[threadIdx.x + o];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) *count = sh[0];
+  int r = 0;
+  for (int k = 0; k < NT / 64; k++) r += shc[k];
+  if (blockIdx.x == 0 && threadIdx.x == 0) *count = r;
+  return r;
 }
 
 // Block-wide (max, sum-exp) combine for a 1024-thread block.
@@ -653,10 +706,10 @@ __device__ inline float block_sum(float v, float* shm) {
 template <int NT, int NV4, typename TOut, bool SMOOTH>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT == 1024 && !SMOOTH ? 8 : 1))) void ce_rows_reg_kernel(
     const float* __restrict__ logits, const int32_t* __restrict__ labels, TOut* __restrict__ dL,
-    float* __restrict__ row_loss, const int* __restrict__ count, int T, int V, int ignoreId,
+    float* __restrict__ row_loss, int* __restrict__ count, int T, int V, int ignoreId,
     float smoothing) {
   __shared__ float shm[4 * NT / 64];
-  const int real = *count;
+  const int real = block_count_labels<NT>(labels, T, ignoreId, count);
   const float scale = real > 0 ? 1.f / (float)real : 0.f;
   const float epsOverV = smoothing / (float)V, oneMinusE = 1.f - smoothing;
   const int c0 = threadIdx.x * 4;  // this thread's column in chunk j is c0 + j*NT*4
@@ -742,10 +795,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT == 1024 &
 template <int NT, typename TOut>
 __global__ __launch_bounds__(NT) void ce_rows_2pass_kernel(
     const float* __restrict__ logits, const int32_t* __restrict__ labels, TOut* __restrict__ dL,
-    float* __restrict__ row_loss, const int* __restrict__ count, int T, int V, int ignoreId,
+    float* __restrict__ row_loss, int* __restrict__ count, int T, int V, int ignoreId,
     float smoothing) {
   __shared__ float shm[2 * NT / 64 + 2 * NT / 64];
-  const int real = *count;
+  const int real = block_count_labels<NT>(labels, T, ignoreId, count);
   const float scale = real > 0 ? 1.f / (float)real : 0.f;
   const float epsOverV = smoothing / (float)V, oneMinusE = 1.f - smoothing;
   for (int t = blockIdx.x; t < T; t += gridDim.x) {
@@ -802,10 +855,10 @@ __device__ __forceinline__ float ce_exp(float x) {
 template <int NT, typename TOut>
 __global__ __launch_bounds__(NT) void ce_rows_2pass_vec_kernel(
     const float* __restrict__ logits, const int32_t* __restrict__ labels, TOut* __restrict__ dL,
-    float* __restrict__ row_loss, const int* __restrict__ count, int T, int V, int ignoreId,
+    float* __restrict__ row_loss, int* __restrict__ count, int T, int V, int ignoreId,
     float smoothing) {
   __shared__ float shm[2 * NT / 64 + 2 * NT / 64];
-  const int real = *count;
+  const int real = block_count_labels<NT>(labels, T, ignoreId, count);
   const float scale = real > 0 ? 1.f / (float)real : 0.f;
   const float epsOverV = smoothing / (float)V, oneMinusE = 1.f - smoothing;
   const int V4 = V / 4;
@@ -889,7 +942,6 @@ static int ce_launch(const float* logits, const int32_t* labels, TOut* dL, float
   if (!ws) return fail(SMHIP_ENOMEM, "cross entropy: workspace");
   int* count = (int*)ws;
   float* row_loss = (float*)(ws + 256);
-  hipLaunchKernelGGL(count_labels_kernel, dim3(1), dim3(1024), 0, s, labels, T, ignoreId, count);
   int G = grid_for(T, 1, 2);
   const bool v4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dL % 16 == 0);
   const bool sm = smoothing > 0.f;

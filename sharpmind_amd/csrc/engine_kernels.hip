@@ -462,7 +462,7 @@ int qkv_prep_backward(const void* dq_, const void* dk_, const void* dv_, int gra
   const bool vec = D == 128 || D == 64;
   // dw partials: one row of 2*D per block, so fewer (larger) blocks when they are needed; the
   // vectorised kernel runs a workgroup per token
-  const int g = vec ? (int)std::min<int64_t>(T, (int64_t)num_cus() * (want_dw ? 2 : 8)) : gridn(rows, 4, 2);
+  const int g = vec ? (int)std::min<int64_t>(T, (int64_t)num_cus() * (want_dw ? 4 : 8)) : gridn(rows, 4, 2);
   float* part = nullptr;
   if (want_dw) {
     part = (float*)workspace(s, sizeof(float) * (size_t)g * 2 * D, 7);
