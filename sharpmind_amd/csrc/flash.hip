@@ -255,25 +255,33 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_fwd_kernel(const uint16_t
         bf16x8 kf = as_bf16x8(*reinterpret_cast<const uint4*>(sK + (j * 32 + (lane & 31)) * KP + kk * 16 + (lane >> 5) * 8));
         sacc[j] = mfma16(kf, qf[kk], sacc[j]);
       }
+    // raw scores: the causal mask only on tiles that reach past the wave's first query, the
+    // log2 scale folded into the exponent (max(s) sl2 = max(s sl2) for sl2 > 0)
     float mx = -INFINITY;
+    if (k0 + KB - 1 > wq_last - 31) {
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+      for (int j = 0; j < 2; j++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const int key = k0 + j * 32 + acc_row(e, lane);
-        float s = key <= qi ? sacc[j][e] * sl2 : -INFINITY;
-        sacc[j][e] = s;
-        mx = fmaxf(mx, s);
-      }
+        for (int e = 0; e < 16; e++) {
+          const int key = k0 + j * 32 + acc_row(e, lane);
+          if (key > qi) sacc[j][e] = -INFINITY;
+          mx = fmaxf(mx, sacc[j][e]);
+        }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) mx = fmaxf(mx, sacc[j][e]);
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(m, mx);
+    const float mnew = fmaxf(m, mx * sl2);
     const float alpha = fexp2(m - mnew);
     float rs = 0.f;
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        float p = fexp2(sacc[j][e] - mnew);
+        float p = fexp2(__builtin_fmaf(sacc[j][e], sl2, -mnew));
         sacc[j][e] = p;
         rs += p;
       }
@@ -369,25 +377,33 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_fwd128_kernel(const uint1
 #pragma unroll
       for (int kk = 0; kk < D / 16; kk++)
         sacc[j] = mfma16(rrow(tK, j * 32 + (lane & 31), kk * 2 + (lane >> 5)), qf[kk], sacc[j]);
+    // raw scores: the causal mask only on tiles that reach past the wave's first query, the
+    // log2 scale folded into the exponent (max(s) sl2 = max(s sl2) for sl2 > 0)
     float mx = -INFINITY;
+    if (k0 + KB - 1 > wq_last - 31) {
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+      for (int j = 0; j < 2; j++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const int key = k0 + j * 32 + acc_row(e, lane);
-        float sv = key <= qi ? sacc[j][e] * sl2 : -INFINITY;
-        sacc[j][e] = sv;
-        mx = fmaxf(mx, sv);
-      }
+        for (int e = 0; e < 16; e++) {
+          const int key = k0 + j * 32 + acc_row(e, lane);
+          if (key > qi) sacc[j][e] = -INFINITY;
+          mx = fmaxf(mx, sacc[j][e]);
+        }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) mx = fmaxf(mx, sacc[j][e]);
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(m, mx);
+    const float mnew = fmaxf(m, mx * sl2);
     const float alpha = fexp2(m - mnew);
     float rs = 0.f;
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        float p = fexp2(sacc[j][e] - mnew);
+        float p = fexp2(__builtin_fmaf(sacc[j][e], sl2, -mnew));
         sacc[j][e] = p;
         rs += p;
       }
