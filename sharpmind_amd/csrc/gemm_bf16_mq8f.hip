@@ -268,7 +268,7 @@ struct FragQ4 {
 };
 
 template <int BM, int BN, int WGM, int NWM, int NWD, int NWL, bool TRANS, bool C_BF16, int ST, int TAG, bool FULL, bool GEN,
-          bool Q4>
+          bool Q4, bool PERS = false>
 __global__ __launch_bounds__(64 * (NWM + NWD + NWL), 1) void gemm_q8f_kernel(Args g) {
   using S = Shape<BM, BN, WGM, NWM>;  // the MFMA waves' layout (epilogue included)
   constexpr int MB = S::MB, NB = S::NB, NT = 64 * (NWM + NWD + NWL);
@@ -287,15 +287,20 @@ __global__ __launch_bounds__(64 * (NWM + NWD + NWL), 1) void gemm_q8f_kernel(Arg
 
   const int ntiles = g.tiles_m * g.tiles_n;
   const int wg = blockIdx.x;
-  int tile = wg;
-  if (ntiles % 8 == 0) tile = (wg % 8) * (ntiles / 8) + wg / 8;
-  constexpr int GM = 8;
-  const int group = tile / (GM * g.tiles_n);
-  const int first_m = group * GM;
-  const int gsz = min(g.tiles_m - first_m, GM);
-  const int tm = first_m + (tile % (GM * g.tiles_n)) % gsz;
-  const int tn = (tile % (GM * g.tiles_n)) / gsz;
-  const int m0 = tm * BM, n0 = tn * BN;
+  // linear index -> tile origin: launch order i goes to XCD i % 8, each XCD owning a contiguous
+  // band of tiles, swept GM m-panels at a time
+  auto tile_origin = [&](int lin, int& om0, int& on0) {
+    int tile = lin;
+    if (ntiles % 8 == 0) tile = (lin % 8) * (ntiles / 8) + lin / 8;
+    constexpr int GM = 8;
+    const int group = tile / (GM * g.tiles_n);
+    const int first_m = group * GM;
+    const int gsz = min(g.tiles_m - first_m, GM);
+    om0 = (first_m + (tile % (GM * g.tiles_n)) % gsz) * BM;
+    on0 = ((tile % (GM * g.tiles_n)) / gsz) * BN;
+  };
+  int m0, n0;
+  tile_origin(wg, m0, n0);
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   // wave-uniform roles: MFMA waves [0, NWM), decoders [NWM, NWM+NWD) (one per SIMD), loaders after
@@ -354,6 +359,79 @@ __global__ __launch_bounds__(64 * (NWM + NWD + NWL), 1) void gemm_q8f_kernel(Arg
     __syncthreads();
     if (role == 0) compute(sA(0), sB(0));
     __syncthreads();
+  }
+  if constexpr (PERS) {
+    // Persistent form (no rank extension, no split): workgroup wg takes tiles wg, wg + G, ... and
+    // runs their K tiles as one sequence u = 0 .. ntl*nk-1, so the copies and the decode of the
+    // next output tile are in flight while the MFMA waves store the previous one.  Every role
+    // passes the same 2 + ntl*nk barriers.
+    static_assert(NWL > 0, "the persistent form has loader waves");
+    const int G = gridDim.x;
+    const int ntl = (ntiles - wg + G - 1) / G;
+    const int nk = nk1, total = ntl * nk;
+    if (total > 0 && role == 2) {
+      LA la;
+      LB lb;
+      auto fetch = [&](int u) {
+        const int kt = u % nk;
+        if (kt == 0) {
+          int fm0, fn0;
+          tile_origin(wg + (u / nk) * G, fm0, fn0);
+          la.init(g.A, fm0, g.M, pl);
+          lb.init(g.B, fn0, g.N, pl);
+        }
+        la.fetch(sA(u % ST), kt * BK, pl);
+        lb.fetch(sQ(u % ST), kt * BK, pl);
+      };
+#pragma unroll
+      for (int u = 0; u < ST - 1; u++)
+        if (u < total) fetch(u);
+      if (total >= ST - 1) wait_vm_n<(ST - 3) * PER>();
+      else wait_vm();
+      ring_barrier();
+      ring_barrier();
+      for (int u = 0; u < total; u++) {
+        if (u + ST - 1 < total) {
+          fetch(u + ST - 1);
+          wait_vm_n<(ST - 3) * PER>();
+        } else {
+          wait_vm();
+        }
+        ring_barrier();
+      }
+    } else if (total > 0 && role == 1) {
+      LB lb;
+      ring_barrier();
+      lb.decode(sQ(0), sB(0), pd);
+      wait_lgkm();
+      ring_barrier();
+      for (int u = 0; u < total; u++) {
+        if (u + 1 < total) {
+          lb.decode(sQ((u + 1) % ST), sB((u + 1) & 1), pd);
+          wait_lgkm();
+        }
+        ring_barrier();
+      }
+    } else if (total > 0) {
+      ring_barrier();
+      ring_barrier();
+      for (int u = 0; u < total; u++) {
+        compute(sA(u % ST), sB(u & 1));
+        if (u % nk == nk - 1) {
+          int em0, en0;
+          tile_origin(wg + (u / nk) * G, em0, en0);
+          gemm_epilogue<S, C_BF16, FULL>(g, acc, em0, en0, 0);
+#pragma unroll
+          for (int i = 0; i < MB; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++)
+#pragma unroll
+              for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+        }
+        ring_barrier();
+      }
+    }
+    return;
   }
   // copies of tiles 0 .. ST-2, then per tile t the copies of tile t+ST-1 and a wait for tile t+2
   // (decoded next, multiplied next-but-one)
@@ -435,6 +513,11 @@ static void launch_q8f_t(const Args& a, int c_bf16, int splits, hipStream_t s) {
   if (a.K2 > 0 && !a.ext_vec) {  // element-wise extension staging, general epilogue
     if (cb) launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, true, ST, TAG, false, true, Q4>, grid, block, s, a);
     else launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, false, ST, TAG, false, true, Q4>, grid, block, s, a);
+  } else if (full && a.K2 == 0 && splits == 1 && !a.partial && a.tiles_m * a.tiles_n >= 4 * num_cus()) {
+    // many tiles per CU and no extension: the persistent form, one workgroup per CU
+    const dim3 pgrid(num_cus() / 8 * 8);
+    if (cb) launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, true, ST, TAG, true, false, Q4, true>, pgrid, block, s, a);
+    else launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, false, ST, TAG, true, false, Q4, true>, pgrid, block, s, a);
   } else if (full) {
     if (cb) launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, true, ST, TAG, true, false, Q4>, grid, block, s, a);
     else launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, false, ST, TAG, true, false, Q4>, grid, block, s, a);
