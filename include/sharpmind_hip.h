@@ -113,6 +113,14 @@ int smhip_qmatmul(int qtype, const float* in, const void* rawW, float* out, int 
  * no backward through quantised weights; this is the dX half of QuantizedMatMulFn's gradient. */
 int smhip_qgemm_bf16(int qtype, int trans_w, int M, int N, int K, const void* A, int64_t lda, const void* rawW,
                      float* C, int64_t ldc, smhip_stream_t stream);
+/* The adapted projection of LoRALayer.Forward (LoRALayer.cs:52-78) through a frozen quantised
+ * base, in one product: C[M,N] = A . deq(W)^T (trans_w as smhip_qgemm_bf16) + alpha2 * A2 . B2^T,
+ * with A2 [M][K2] bf16 (row stride lda2, the u = x A rows) and B2 the rank operand in bf16:
+ * b2_mode 2 = [N][K2] k-contiguous, 3 = [K2][N] (the reference's B [rank, out]), row stride ldb2.
+ * K % 64 == 0, N % 32 == 0; C fp32. */
+int smhip_qgemm_bf16_lora(int qtype, int trans_w, int M, int N, int K, const void* A, int64_t lda, const void* rawW,
+                          int K2, const void* A2, int64_t lda2, int b2_mode, const void* B2, int64_t ldb2,
+                          float alpha2, float* C, int64_t ldc, smhip_stream_t stream);
 
 /* Bit-exact dequantisation of a reference-layout stream of n elements
  * (ReadQ8_0_Scalar QuantizationKernels.Q8.cs:412-433, ReadQ4K_Scalar QuantizationKernels.Q4.cs:951-981). */

@@ -331,6 +331,38 @@ int smhip_qgemm_bf16(int qtype, int trans_w, int M, int N, int K, const void* A,
   return rc;
 }
 
+int smhip_qgemm_bf16_lora(int qtype, int trans_w, int M, int N, int K, const void* A, int64_t lda, const void* rawW,
+                          int K2, const void* A2, int64_t lda2, int b2_mode, const void* B2, int64_t ldb2,
+                          float alpha2, float* C, int64_t ldc, smhip_stream_t stream) {
+  SMHIP_REQUIRE(M >= 0 && N > 0 && K > 0 && A && rawW && C, "qgemm_bf16_lora: bad arguments");
+  SMHIP_REQUIRE(qtype == SMHIP_QTYPE_Q8_0 || qtype == SMHIP_QTYPE_Q4_K, "qgemm_bf16_lora: qtype must be 8 (Q8_0) or 12 (Q4_K)");
+  SMHIP_REQUIRE(K % 64 == 0 && N % 32 == 0, "qgemm_bf16_lora: K must be a multiple of 64 and N of 32");
+  SMHIP_REQUIRE(K2 > 0 && A2 && B2 && (b2_mode == 2 || b2_mode == 3), "qgemm_bf16_lora: bad rank operands");
+  hipStream_t s = STREAM(stream);
+  const int64_t n = (int64_t)N * K;
+  const int64_t row = trans_w ? N : K;
+  if (qtype == SMHIP_QTYPE_Q4_K) SMHIP_REQUIRE(row % 256 == 0, "qgemm_bf16_lora: Q4_K rows must hold whole 256-element super-blocks");
+  void* planes = workspace(s, planes_bytes(qtype, n, nullptr), 5);
+  if (!planes) return fail(SMHIP_ENOMEM, "qgemm_bf16_lora: workspace");
+  QuantPlanes qp;
+  if (int rc = repack_planes(qtype, rawW, n, planes, &qp, s)) return rc;
+  void* fr = workspace(s, frag_planes_bytes(n, qtype), 8);
+  if (!fr) return fail(SMHIP_ENOMEM, "qgemm_bf16_lora: workspace");
+  GemmArgs g{};
+  g.precision = SMHIP_PREC_BF16;
+  g.split_k = 1;
+  g.alpha = 1.f;
+  g.M = M; g.N = N; g.K = K;
+  g.A = {SRC_BF16_K, A, nullptr, lda};
+  if (int rc = make_frag_planes(qp, trans_w ? K : N, trans_w ? N : K, trans_w, fr, &g.B, s)) return rc;
+  g.K2 = K2;
+  g.A2 = {SRC_BF16_K, A2, nullptr, lda2};
+  g.B2 = {b2_mode == 2 ? SRC_BF16_K : SRC_BF16_R, B2, nullptr, ldb2};
+  g.alpha2 = alpha2;
+  g.C = C; g.ldc = ldc;
+  return gemm(g, s);
+}
+
 int smhip_dequant(int qtype, const void* raw, float* out, int64_t n, smhip_stream_t stream) {
   SMHIP_REQUIRE(n >= 0 && (n == 0 || (raw && out)), "dequant: bad arguments");
   return dequant_raw(qtype, raw, out, n, STREAM(stream));

@@ -313,9 +313,9 @@ __device__ __forceinline__ uint4 scale_bf8(uint4 v, float mult) {
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 template <int ROWS, int NT>
-__device__ __forceinline__ void ext_tile_k(const Op& o, int r0, int k0, int R, int K, float mult, uint8_t* lds) {
+__device__ __forceinline__ void ext_tile_k(const Op& o, int r0, int k0, int R, int K, float mult, uint8_t* lds, int tid) {
   const uint16_t* p = (const uint16_t*)o.p;
-  for (int c = threadIdx.x; c < ROWS * 8; c += NT) {
+  for (int c = tid; c < ROWS * 8; c += NT) {
     const int r = c >> 3, ch = c & 7, k = k0 + ch * 8;
     uint4 v = make_uint4(0, 0, 0, 0);
     if (r0 + r < R && k < K) v = scale_bf8(*reinterpret_cast<const uint4*>(p + (int64_t)(r0 + r) * o.ld + k), mult);
@@ -323,9 +323,9 @@ __device__ __forceinline__ void ext_tile_k(const Op& o, int r0, int k0, int R, i
   }
 }
 template <int ROWS, int NT>
-__device__ __forceinline__ void ext_tile_r(const Op& o, int r0, int k0, int R, int K, float mult, uint8_t* lds) {
+__device__ __forceinline__ void ext_tile_r(const Op& o, int r0, int k0, int R, int K, float mult, uint8_t* lds, int tid) {
   const uint16_t* p = (const uint16_t*)o.p;
-  for (int c = threadIdx.x; c < ROWS; c += NT) {  // (8-row group, 8-k chunk)
+  for (int c = tid; c < ROWS; c += NT) {  // (8-row group, 8-k chunk)
     const int rg = c % (ROWS / 8), ch = c / (ROWS / 8), kb = k0 + ch * 8;
     uint32_t w[8][4];
 #pragma unroll
@@ -347,8 +347,8 @@ __device__ __forceinline__ void ext_tile_r(const Op& o, int r0, int k0, int R, i
 template <int ROWS, int NT>
 __device__ __forceinline__ void ext_tile(int mode, bool vec, const Op& o, int r0, int k0, int R, int K, float mult,
                                          uint8_t* lds) {
-  if (vec && mode == SRC_BF16_K) ext_tile_k<ROWS, NT>(o, r0, k0, R, K, mult, lds);
-  else if (vec && mode == SRC_BF16_R) ext_tile_r<ROWS, NT>(o, r0, k0, R, K, mult, lds);
+  if (vec && mode == SRC_BF16_K) ext_tile_k<ROWS, NT>(o, r0, k0, R, K, mult, lds, threadIdx.x);
+  else if (vec && mode == SRC_BF16_R) ext_tile_r<ROWS, NT>(o, r0, k0, R, K, mult, lds, threadIdx.x);
   else gen_tile<ROWS, NT>(mode, o, r0, k0, R, K, mult, lds);
 }
 

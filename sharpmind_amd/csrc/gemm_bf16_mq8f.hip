@@ -163,8 +163,8 @@ struct FragQ8 {
 template <int ROWS, int NT, bool GEN>
 __device__ __forceinline__ void ext_stage(int mode, const Op& o, int r0, int k0, int R, int K, float mult, uint8_t* lds) {
   if constexpr (GEN) gen_tile<ROWS, NT>(mode, o, r0, k0, R, K, mult, lds);
-  else if (mode == SRC_BF16_K) ext_tile_k<ROWS, NT>(o, r0, k0, R, K, mult, lds);
-  else ext_tile_r<ROWS, NT>(o, r0, k0, R, K, mult, lds);
+  else if (mode == SRC_BF16_K) ext_tile_k<ROWS, NT>(o, r0, k0, R, K, mult, lds, threadIdx.x);
+  else ext_tile_r<ROWS, NT>(o, r0, k0, R, K, mult, lds, threadIdx.x);
 }
 
 // Q4_K fragment planes: raw stage = BN*32 code bytes (32 per row of a 32 x 64 block) and BN*16
@@ -350,66 +350,72 @@ __global__ __launch_bounds__(64 * (NWM + NWD + NWL), 1) void gemm_q8f_kernel(Arg
   // landed; tile 0 decoded), one after each tile.  The loaders are the only waves with copies in
   // flight: an LDS copy also counts against the issuing wave's LDS counter, so a wave that waited
   // for its own LDS reads would drain the ring.
-  // rank extension (LoRA) first, from stage 0 and decoded buffer 0: every thread stages, the MFMA
-  // waves multiply.  The accumulators are live through the role loops that follow, which the
-  // 168-register budget of a 10-wave workgroup holds without spilling.
-  for (int t = 0; t < nk2; t++) {
-    ext_stage<BM, NT, GEN>(g.amode2, g.A2, m0, t * BK, g.M, g.K2, g.alpha2, sA(0));
-    ext_stage<BN, NT, GEN>(g.bmode2, g.B2, n0, t * BK, g.N, g.K2, 1.f, sB(0));
-    __syncthreads();
-    if (role == 0) compute(sA(0), sB(0));
-    __syncthreads();
-  }
   if constexpr (PERS) {
-    // Persistent form (no rank extension, no split): workgroup wg takes tiles wg, wg + G, ... and
-    // runs their K tiles as one sequence u = 0 .. ntl*nk-1, so the copies and the decode of the
-    // next output tile are in flight while the MFMA waves store the previous one.  Every role
-    // passes the same 2 + ntl*nk barriers.
-    static_assert(NWL > 0, "the persistent form has loader waves");
+    // Persistent form (no split; at most one rank-extension K tile, element-wise staging not
+    // used): workgroup wg takes output tiles wg, wg + G, ... and runs their K tiles as one
+    // sequence u = 0 .. ntl*sp-1 (sp = main K tiles + the extension tile, last), so the copies
+    // and the decode of the next output tile are in flight while the MFMA waves store the
+    // previous one.  The extension tile has no copies: the decoder waves stage its two operands
+    // into the ring stage and the decoded buffer it would have used.  Every role passes the same
+    // 2 + ntl*sp barriers.
+    static_assert(NWL > 0 && ST == 4 && !GEN, "persistent form: loader waves, a 4-stage ring");
     const int G = gridDim.x;
     const int ntl = (ntiles - wg + G - 1) / G;
-    const int nk = nk1, total = ntl * nk;
+    const int nk = nk1, sp = nk1 + nk2, total = ntl * sp;
+    auto is_ext = [&](int u) { return u % sp >= nk; };
     if (total > 0 && role == 2) {
       LA la;
       LB lb;
       auto fetch = [&](int u) {
-        const int kt = u % nk;
+        const int kt = u % sp;
+        if (kt >= nk) return;
         if (kt == 0) {
           int fm0, fn0;
-          tile_origin(wg + (u / nk) * G, fm0, fn0);
+          tile_origin(wg + (u / sp) * G, fm0, fn0);
           la.init(g.A, fm0, g.M, pl);
           lb.init(g.B, fn0, g.N, pl);
         }
         la.fetch(sA(u % ST), kt * BK, pl);
         lb.fetch(sQ(u % ST), kt * BK, pl);
       };
+      // steps up to v issued: step v - 1 (and older) landed; v itself may be in flight when it
+      // has copies (loads complete in order)
+      auto wait_upto = [&](int v) {
+        if (v < total && !is_ext(v)) wait_vm_n<PER>();
+        else wait_vm();
+      };
 #pragma unroll
       for (int u = 0; u < ST - 1; u++)
         if (u < total) fetch(u);
-      if (total >= ST - 1) wait_vm_n<(ST - 3) * PER>();
-      else wait_vm();
+      wait_upto(ST - 2);
       ring_barrier();
       ring_barrier();
       for (int u = 0; u < total; u++) {
-        if (u + ST - 1 < total) {
-          fetch(u + ST - 1);
-          wait_vm_n<(ST - 3) * PER>();
-        } else {
-          wait_vm();
-        }
+        if (u + ST - 1 < total) fetch(u + ST - 1);
+        wait_upto(u + ST - 1);
         ring_barrier();
       }
     } else if (total > 0 && role == 1) {
       LB lb;
+      auto prep = [&](int u) {  // step u's B tile (and, for the extension, its A tile)
+        if (is_ext(u)) {
+          int em0, en0;
+          tile_origin(wg + (u / sp) * G, em0, en0);
+          const int tid = pd, k0 = (u % sp - nk) * BK;
+          if (g.amode2 == SRC_BF16_K) ext_tile_k<BM, 64 * NWD>(g.A2, em0, k0, g.M, g.K2, g.alpha2, sA(u % ST), tid);
+          else ext_tile_r<BM, 64 * NWD>(g.A2, em0, k0, g.M, g.K2, g.alpha2, sA(u % ST), tid);
+          if (g.bmode2 == SRC_BF16_K) ext_tile_k<BN, 64 * NWD>(g.B2, en0, k0, g.N, g.K2, 1.f, sB(u & 1), tid);
+          else ext_tile_r<BN, 64 * NWD>(g.B2, en0, k0, g.N, g.K2, 1.f, sB(u & 1), tid);
+        } else {
+          lb.decode(sQ(u % ST), sB(u & 1), pd);
+        }
+        wait_lgkm();
+      };
       ring_barrier();
-      lb.decode(sQ(0), sB(0), pd);
-      wait_lgkm();
+      prep(0);
       ring_barrier();
       for (int u = 0; u < total; u++) {
-        if (u + 1 < total) {
-          lb.decode(sQ((u + 1) % ST), sB((u + 1) & 1), pd);
-          wait_lgkm();
-        }
+        if (u + 1 < total) prep(u + 1);
         ring_barrier();
       }
     } else if (total > 0) {
@@ -417,9 +423,9 @@ __global__ __launch_bounds__(64 * (NWM + NWD + NWL), 1) void gemm_q8f_kernel(Arg
       ring_barrier();
       for (int u = 0; u < total; u++) {
         compute(sA(u % ST), sB(u & 1));
-        if (u % nk == nk - 1) {
+        if (u % sp == sp - 1) {
           int em0, en0;
-          tile_origin(wg + (u / nk) * G, em0, en0);
+          tile_origin(wg + (u / sp) * G, em0, en0);
           gemm_epilogue<S, C_BF16, FULL>(g, acc, em0, en0, 0);
 #pragma unroll
           for (int i = 0; i < MB; i++)
@@ -432,6 +438,16 @@ __global__ __launch_bounds__(64 * (NWM + NWD + NWL), 1) void gemm_q8f_kernel(Arg
       }
     }
     return;
+  }
+  // rank extension (LoRA) first, from stage 0 and decoded buffer 0: every thread stages, the MFMA
+  // waves multiply.  The accumulators are live through the role loops that follow, which the
+  // 168-register budget of a 10-wave workgroup holds without spilling.
+  for (int t = 0; t < nk2; t++) {
+    ext_stage<BM, NT, GEN>(g.amode2, g.A2, m0, t * BK, g.M, g.K2, g.alpha2, sA(0));
+    ext_stage<BN, NT, GEN>(g.bmode2, g.B2, n0, t * BK, g.N, g.K2, 1.f, sB(0));
+    __syncthreads();
+    if (role == 0) compute(sA(0), sB(0));
+    __syncthreads();
   }
   // copies of tiles 0 .. ST-2, then per tile t the copies of tile t+ST-1 and a wait for tile t+2
   // (decoded next, multiplied next-but-one)
@@ -513,8 +529,8 @@ static void launch_q8f_t(const Args& a, int c_bf16, int splits, hipStream_t s) {
   if (a.K2 > 0 && !a.ext_vec) {  // element-wise extension staging, general epilogue
     if (cb) launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, true, ST, TAG, false, true, Q4>, grid, block, s, a);
     else launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, false, ST, TAG, false, true, Q4>, grid, block, s, a);
-  } else if (full && a.K2 == 0 && splits == 1 && !a.partial && a.tiles_m * a.tiles_n >= 4 * num_cus()) {
-    // many tiles per CU and no extension: the persistent form, one workgroup per CU
+  } else if (full && a.K2 <= BK && splits == 1 && !a.partial && a.tiles_m * a.tiles_n >= 4 * num_cus()) {
+    // many tiles per CU: the persistent form, one workgroup per CU
     const dim3 pgrid(num_cus() / 8 * 8);
     if (cb) launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, true, ST, TAG, true, false, Q4, true>, pgrid, block, s, a);
     else launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, false, ST, TAG, true, false, Q4, true>, pgrid, block, s, a);

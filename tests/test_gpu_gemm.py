@@ -88,6 +88,54 @@ def test_qgemm_bf16(orc, dev, qtype, trans, M, N, K):
     assert rel_err(tc.cpu().numpy(), ref) <= 1e-5, rel_err(tc.cpu().numpy(), ref)
 
 
+def _quant(orc, qtype, w):
+    if qtype == 8:
+        raw = np.zeros(w.size // 32 * 34, np.uint8)
+        assert orc.orc_quantize_q8_0(w, w.size, raw) == 0
+        deq = np.zeros_like(w)
+        orc.orc_dequant_q8_0(raw, deq, w.size)
+    else:
+        raw = np.zeros(w.size // 256 * 144, np.uint8)
+        assert orc.orc_quantize_q4k(w, w.size, raw) == 0
+        deq = np.zeros_like(w)
+        orc.orc_dequant_q4k(raw, deq, w.size)
+    return raw, deq
+
+
+@pytest.mark.parametrize("qtype", [8, 12])
+@pytest.mark.parametrize("trans,b2_mode", [(0, 3), (1, 2)])
+@pytest.mark.parametrize("M,N,K,K2", [(300, 256, 512, 48), (1024, 16384, 256, 16), (1536, 12544, 512, 32),
+                                      (2048, 8192, 256, 64)])
+def test_qgemm_bf16_lora(orc, dev, qtype, trans, b2_mode, M, N, K, K2):
+    """The adapted projection in one product, C = A deq(W)^T + s A2 B2^T (LoRALayer.Forward with
+    A2 = x A): the rank operand rides as one extra K tile.  The first shape runs one output tile
+    per workgroup (extension first); the others have at least four tiles per CU and take the
+    persistent form, where the extension is the last K tile of each output tile and is staged by
+    the decoder waves.  Forward form with the reference's B [rank, out] layout, dX form with the
+    k-contiguous A operand, both base formats; float64 reference on bf16-rounded operands."""
+    if qtype == 12 and (N if trans else K) % 256:
+        pytest.skip("Q4_K blocks are 256 weights along the quantised axis")
+    rng = np.random.default_rng(M + N + K + K2 + qtype + trans)
+    shape = (K, N) if trans else (N, K)
+    raw, deq = _quant(orc, qtype, (rng.standard_normal(shape) * 0.05).astype(np.float32).ravel())
+    wb = torch.from_numpy(deq).to(torch.bfloat16).float().numpy().reshape(shape).astype(np.float64)
+    a = _rnd((M, K), rng)
+    a2 = _rnd((M, K2), rng)
+    b2 = _rnd((N, K2), rng)  # B2^T rows
+    s2 = 0.5  # the engine scales A2 by alpha/rank when staging it in bf16: a power of two is exact
+    ta, ta2 = (torch.from_numpy(x).to(dev).to(torch.bfloat16) for x in (a, a2))
+    tb2 = torch.from_numpy(np.ascontiguousarray(b2 if b2_mode == 2 else b2.T)).to(dev).to(torch.bfloat16)
+    ldb2 = K2 if b2_mode == 2 else N
+    tc = torch.zeros(M, N, device=dev)
+    check(sharpmind_amd.lib().smhip_qgemm_bf16_lora(qtype, trans, M, N, K, ta.data_ptr(), K,
+                                                    torch.from_numpy(raw).to(dev).data_ptr(), K2, ta2.data_ptr(), K2,
+                                                    b2_mode, tb2.data_ptr(), ldb2, s2, tc.data_ptr(), N,
+                                                    torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    ref = a.astype(np.float64) @ (wb if trans else wb.T) + s2 * (a2.astype(np.float64) @ b2.astype(np.float64).T)
+    assert rel_err(tc.cpu().numpy(), ref) <= 1e-5, rel_err(tc.cpu().numpy(), ref)
+
+
 @pytest.mark.parametrize("M,N,K,am,bm", [(6144, 32, 4096, 3, 3), (4096, 48, 4096, 2, 2), (1024, 16, 4096, 3, 3),
                                          (48, 4096, 4096, 2, 2), (4096, 48, 1024, 2, 3), (4100, 16, 3072, 2, 3),
                                          (4096, 32, 6144, 2, 2), (2000, 64, 1152, 2, 2), (16, 1000, 640, 2, 2),
