@@ -121,6 +121,14 @@ int smhip_qgemm_bf16(int qtype, int trans_w, int M, int N, int K, const void* A,
 int smhip_qgemm_bf16_lora(int qtype, int trans_w, int M, int N, int K, const void* A, int64_t lda, const void* rawW,
                           int K2, const void* A2, int64_t lda2, int b2_mode, const void* B2, int64_t ldb2,
                           float alpha2, float* C, int64_t ldc, smhip_stream_t stream);
+/* Tied LM head forward and cross-entropy backward in bf16 (BackpropEngine.cs:889-907 head,
+ * CrossEntropyLoss.Compute/Backward with mean over labels != -100): logits[T,V] = x[T,d] . deq(E)^T
+ * (x bf16, E the Q8_0 / Q4_K embedding table [V][d] in the reference byte layout, logits fp32),
+ * dlogits = (softmax - onehot) / count in bf16, *loss = mean loss (loss may be null).  When the
+ * product has at least four 128x128 tiles per CU the GEMM also emits softmax row statistics and
+ * the logits are read once by the cross-entropy. */
+int smhip_lm_head_ce_bf16(int qtype, int T, int V, int d, const void* x, const void* rawE, const int32_t* labels,
+                          float* logits, void* dlogits, float* loss, smhip_stream_t stream);
 
 /* Bit-exact dequantisation of a reference-layout stream of n elements
  * (ReadQ8_0_Scalar QuantizationKernels.Q8.cs:412-433, ReadQ4K_Scalar QuantizationKernels.Q4.cs:951-981). */

@@ -363,6 +363,39 @@ int smhip_qgemm_bf16_lora(int qtype, int trans_w, int M, int N, int K, const voi
   return gemm(g, s);
 }
 
+int smhip_lm_head_ce_bf16(int qtype, int T, int V, int d, const void* x, const void* rawE, const int32_t* labels,
+                          float* logits, void* dlogits, float* loss, smhip_stream_t stream) {
+  SMHIP_REQUIRE(T > 0 && V > 0 && d > 0 && x && rawE && labels && logits && dlogits, "lm_head_ce_bf16: bad arguments");
+  SMHIP_REQUIRE(qtype == SMHIP_QTYPE_Q8_0 || qtype == SMHIP_QTYPE_Q4_K, "lm_head_ce_bf16: qtype must be 8 (Q8_0) or 12 (Q4_K)");
+  SMHIP_REQUIRE(d % 64 == 0 && V % 64 == 0, "lm_head_ce_bf16: d and V must be multiples of 64");
+  if (qtype == SMHIP_QTYPE_Q4_K) SMHIP_REQUIRE(d % 256 == 0, "lm_head_ce_bf16: Q4_K rows must hold whole super-blocks");
+  hipStream_t s = STREAM(stream);
+  const int64_t n = (int64_t)V * d;
+  void* planes = workspace(s, planes_bytes(qtype, n, nullptr), 5);
+  void* fr = workspace(s, frag_planes_bytes(n, qtype), 8);
+  if (!planes || !fr) return fail(SMHIP_ENOMEM, "lm_head_ce_bf16: workspace");
+  QuantPlanes qp;
+  if (int rc = repack_planes(qtype, rawE, n, planes, &qp, s)) return rc;
+  GemmArgs g{};
+  g.precision = SMHIP_PREC_BF16;
+  g.split_k = 1;
+  g.alpha = 1.f;
+  g.M = T; g.N = V; g.K = d;
+  g.A = {SRC_BF16_K, x, nullptr, d};
+  if (int rc = make_frag_planes(qp, V, d, 0, fr, &g.B, s)) return rc;
+  g.C = logits; g.ldc = V;
+  // the head GEMM's softmax row statistics when its persistent form applies
+  const bool stats = T % 128 == 0 && V % 128 == 0 && (int64_t)(T / 128) * (V / 128) >= 4 * num_cus() &&
+                     ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dlogits % 16 == 0);
+  if (stats) {
+    g.rowstat = (float*)workspace(s, sizeof(float) * 2 * (size_t)T * (V / 64), 9);
+    if (!g.rowstat) return fail(SMHIP_ENOMEM, "lm_head_ce_bf16: workspace");
+  }
+  if (int rc = gemm(g, s)) return rc;
+  if (stats) return ce_softmax_grad_bf16_stats(logits, g.rowstat, V / 64, labels, (uint16_t*)dlogits, loss, T, V, -100, s);
+  return ce_softmax_grad_bf16(logits, labels, (uint16_t*)dlogits, loss, T, V, -100, 0.f, s);
+}
+
 int smhip_dequant(int qtype, const void* raw, float* out, int64_t n, smhip_stream_t stream) {
   SMHIP_REQUIRE(n >= 0 && (n == 0 || (raw && out)), "dequant: bad arguments");
   return dequant_raw(qtype, raw, out, n, STREAM(stream));

@@ -188,6 +188,9 @@ struct GemmArgs {
   int* masked;
   // rank-sized products: hold the launch so the next product with this hold shares it
   struct SkinnyHold* hold;
+  // softmax row statistics of C (fp32 C, fragment-plane B, whole 128x128 tiles, at least four per
+  // CU): per row and block of 64 columns the pair (max, sum_c exp(C - max)), [M][N/64][2]
+  float* rowstat;
 };
 int gemm(const GemmArgs& g, hipStream_t s);
 

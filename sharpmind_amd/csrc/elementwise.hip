@@ -852,11 +852,14 @@ __device__ __forceinline__ float ce_exp(float x) {
   if constexpr (sizeof(TOut) == 2) return __expf(x);
   else return expf(x);
 }
+// stats (optional, no smoothing): per row nst pairs (max, sum exp(z - max)) over consecutive
+// column blocks, written by the logits' producer; pass 1 then combines them instead of reading
+// the row, and the logits are read once.
 template <int NT, typename TOut>
 __global__ __launch_bounds__(NT) void ce_rows_2pass_vec_kernel(
     const float* __restrict__ logits, const int32_t* __restrict__ labels, TOut* __restrict__ dL,
     float* __restrict__ row_loss, int* __restrict__ count, int T, int V, int ignoreId,
-    float smoothing) {
+    float smoothing, const float* __restrict__ stats, int nst) {
   __shared__ float shm[2 * NT / 64 + 2 * NT / 64];
   const int real = block_count_labels<NT>(labels, T, ignoreId, count);
   const float scale = real > 0 ? 1.f / (float)real : 0.f;
@@ -872,7 +875,19 @@ __global__ __launch_bounds__(NT) void ce_rows_2pass_vec_kernel(
       continue;
     }
     float m = -INFINITY, sum = 0.f, zsum = 0.f;
-    for (int c4 = threadIdx.x; c4 < V4; c4 += NT) {
+    if (stats) {
+      const float2* st = reinterpret_cast<const float2*>(stats) + (int64_t)t * nst;
+      for (int b = threadIdx.x; b < nst; b += NT) {
+        const float2 q = st[b];
+        if (q.x > m) {
+          sum = sum * ce_exp<TOut>(m - q.x) + q.y;
+          m = q.x;
+        } else {
+          sum += q.y * ce_exp<TOut>(q.x - m);
+        }
+      }
+    }
+    for (int c4 = threadIdx.x; c4 < (stats ? 0 : V4); c4 += NT) {
       const float4 v = ld4(z + 4 * c4);
       zsum += (v.x + v.y) + (v.z + v.w);
       const float mx = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
@@ -936,7 +951,7 @@ __global__ __launch_bounds__(1024) void mean_loss_kernel(const float* __restrict
 
 template <typename TOut>
 static int ce_launch(const float* logits, const int32_t* labels, TOut* dL, float* loss, int T, int V,
-                     int ignoreId, float smoothing, hipStream_t s) {
+                     int ignoreId, float smoothing, hipStream_t s, const float* stats = nullptr, int nst = 0) {
   if (T <= 0) return SMHIP_OK;
   char* ws = (char*)workspace(s, 256 + sizeof(float) * (size_t)T, 1);
   if (!ws) return fail(SMHIP_ENOMEM, "cross entropy: workspace");
@@ -945,7 +960,10 @@ static int ce_launch(const float* logits, const int32_t* labels, TOut* dL, float
   int G = grid_for(T, 1, 2);
   const bool v4 = (V % 4 == 0) && ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dL % 16 == 0);
   const bool sm = smoothing > 0.f;
-  if (v4 && V <= 1024 * 4 * 8 && V > 256 * 4 * 8) {
+  if (stats) {
+    SMHIP_REQUIRE(v4 && smoothing == 0.f && nst > 0, "cross entropy: precomputed row statistics need float4 rows and no smoothing");
+    hipLaunchKernelGGL((ce_rows_2pass_vec_kernel<1024, TOut>), dim3(G), dim3(1024), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing, stats, nst);
+  } else if (v4 && V <= 1024 * 4 * 8 && V > 256 * 4 * 8) {
     if (sm) hipLaunchKernelGGL((ce_rows_reg_kernel<1024, 8, TOut, true>), dim3(G), dim3(1024), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
     else hipLaunchKernelGGL((ce_rows_reg_kernel<1024, 8, TOut, false>), dim3(G), dim3(1024), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
   } else if (v4 && V <= 256 * 4 * 8) {
@@ -953,7 +971,7 @@ static int ce_launch(const float* logits, const int32_t* labels, TOut* dL, float
     else hipLaunchKernelGGL((ce_rows_reg_kernel<256, 8, TOut, false>), dim3(G), dim3(256), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
   }
   else if (v4)
-    hipLaunchKernelGGL((ce_rows_2pass_vec_kernel<1024, TOut>), dim3(G), dim3(1024), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
+    hipLaunchKernelGGL((ce_rows_2pass_vec_kernel<1024, TOut>), dim3(G), dim3(1024), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing, nullptr, 0);
   else
     hipLaunchKernelGGL((ce_rows_2pass_kernel<1024, TOut>), dim3(G), dim3(1024), 0, s, logits, labels, dL, row_loss, count, T, V, ignoreId, smoothing);
   SMHIP_CHECK_LAUNCH();
@@ -971,6 +989,10 @@ int ce_softmax_grad(const float* logits, const int32_t* labels, float* dL, float
 int ce_softmax_grad_bf16(const float* logits, const int32_t* labels, uint16_t* dL, float* loss,
                          int T, int V, int ignoreId, float smoothing, hipStream_t s) {
   return ce_launch<uint16_t>(logits, labels, dL, loss, T, V, ignoreId, smoothing, s);
+}
+int ce_softmax_grad_bf16_stats(const float* logits, const float* stats, int nst, const int32_t* labels, uint16_t* dL,
+                               float* loss, int T, int V, int ignoreId, hipStream_t s) {
+  return ce_launch<uint16_t>(logits, labels, dL, loss, T, V, ignoreId, 0.f, s, stats, nst);
 }
 
 // ============================================================================

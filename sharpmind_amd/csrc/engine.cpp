@@ -98,6 +98,9 @@ struct Engine {
   // activations
   std::vector<Saved> sv;
   float *h_fin, *rinv_f, *logits, *cosT, *sinT, *loss, *gnorm;
+  // bf16 LoRA engines on fragment planes: the head GEMM's softmax row statistics ([T][V/64] pairs),
+  // so cross-entropy reads the logits once (null: cross-entropy computes them itself)
+  float* rowstat = nullptr;
   void *xnf, *dlogits;
   // backward work
   float *dh, *dx, *dq, *dk, *dv;
@@ -338,6 +341,10 @@ static int build(Engine* e) {
   e->xnf = dalloc(e, ES * (size_t)T * d);
   e->logits = (float*)dalloc(e, sizeof(float) * (size_t)T * V);
   e->dlogits = e->bf ? dalloc(e, 2 * (size_t)T * V) : (void*)e->logits;  // fp32 mode: in place
+  if (e->bf && e->frag && T % 128 == 0 && V % 128 == 0 && (int64_t)(T / 128) * (V / 128) >= 4 * num_cus()) {
+    e->rowstat = (float*)dalloc(e, sizeof(float) * 2 * (size_t)T * (V / 64));
+    if (!e->rowstat) return fail(SMHIP_ENOMEM, "engine: row statistics");
+  }
   e->cosT = (float*)dalloc(e, sizeof(float) * (size_t)c.seq * c.head_dim / 2);
   e->sinT = (float*)dalloc(e, sizeof(float) * (size_t)c.seq * c.head_dim / 2);
   e->loss = (float*)dalloc(e, 256);
@@ -610,10 +617,12 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
     else if (e->lora) g.B = Operand{e->emb_q.kind == SMHIP_QTYPE_Q8_0 ? SRC_Q8_K : SRC_Q4K_K, e->emb_q.qs, e->emb_q.sc, d};
     else g.B = e->emb.bf ? Operand{SRC_BF16_K, e->emb.bf, nullptr, d} : Operand{SRC_F32_K, e->emb.data, nullptr, d};
     g.C = e->logits; g.ldc = V;
+    g.rowstat = e->rowstat;
     R_(gemm(g, s));
   }
   // loss + dLogits (CrossEntropyLoss.Compute / Backward, TrainLoop.cs:233-237)
-  if (e->bf) R_(ce_softmax_grad_bf16(e->logits, labels, (uint16_t*)e->dlogits, e->loss, T, V, -100, 0.f, s));
+  if (e->rowstat) R_(ce_softmax_grad_bf16_stats(e->logits, e->rowstat, V / 64, labels, (uint16_t*)e->dlogits, e->loss, T, V, -100, s));
+  else if (e->bf) R_(ce_softmax_grad_bf16(e->logits, labels, (uint16_t*)e->dlogits, e->loss, T, V, -100, 0.f, s));
   else R_(ce_softmax_grad(e->logits, labels, (float*)e->dlogits, e->loss, T, V, -100, 0.f, s));
 
   // ---------------- backward

@@ -402,6 +402,7 @@ int gemm(const GemmArgs& g, hipStream_t s) {
     if (fast < 0) return fast;
     if (fast > 0) return SMHIP_OK;
   }
+  SMHIP_REQUIRE(!g.rowstat, "gemm: softmax row statistics need the persistent fragment-plane path");
   SMHIP_REQUIRE(g.A.mode < SRC_Q8T && g.B.mode < SRC_Q8T,
                 "gemm: column-plane operands need the bf16 MFMA path (bf16 precision, K a multiple of 64)");
   SMHIP_REQUIRE(!(g.R && g.c_bf16), "gemm: residual input needs fp32 output");

@@ -256,6 +256,13 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
   a.tiles_m = ceil_div(g.M, kTiles[tile].bm);
   a.tiles_n = ceil_div(g.N, kTiles[tile].bn);
   a.partial = nullptr;
+  a.rowstat = g.rowstat;
+  if (g.rowstat) {
+    SMHIP_REQUIRE(frag && sp == 1 && g.K2 == 0 && !g.c_bf16 && !g.bias && !g.R && g.beta == 0.f && g.M % 128 == 0 &&
+                      g.N % 128 == 0 && (int64_t)a.tiles_m * a.tiles_n >= 4 * num_cus(),
+                  "gemm: softmax row statistics need the persistent fragment-plane form (fp32 C, whole tiles, "
+                  "at least four per CU, no extension)");
+  }
   if (sp > 1) {
     a.partial = (float*)workspace(s, sizeof(float) * (size_t)sp * g.M * g.N, 3);
     if (!a.partial) return fail(SMHIP_ENOMEM, "gemm: split-K workspace");

@@ -366,6 +366,7 @@ struct Args {
   int tiles_m, tiles_n;
   int kps;          // main K tiles per split (blockIdx.y = split)
   float* partial;   // non-null: write raw partial sums [split][M][N] instead of C
+  float* rowstat;   // non-null (persistent fragment-plane form only): per row and 64 columns, (max, sum exp(c - max)) of C
 };
 
 template <int BM, int BN, int WGM, int NW, int ST = 2>

@@ -267,8 +267,52 @@ struct FragQ4 {
   }
 };
 
+// Epilogue of a transposed accumulator tile (STAT): block acc[i][j] holds rows wm*WM + i*32 +
+// lane%32 of C and its columns wn*WN + j*32 + acc_row(e).  C = alpha * acc is stored 16 bytes at a
+// time, and each (row, 64 columns of the wave) gets its softmax statistics: the lane's 32 values
+// and those of lane ^ 32 (the other half of the columns) give (max, sum exp(c - max)) with the
+// hardware exponential.
+template <class S>
+__device__ __forceinline__ void stat_epilogue(const Args& g, floatx16 (&acc)[S::MB][S::NB], int m0, int n0) {
+  static_assert(S::WN == 64, "one statistics pair per wave and row");
+  constexpr int MB = S::MB, NB = S::NB;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int wm = wv / S::WGN, wn = wv % S::WGN;
+  const int nst = g.N / 64;
+#pragma unroll
+  for (int i = 0; i < MB; i++) {
+    const int64_t row = m0 + wm * S::WM + i * 32 + (lane & 31);
+    float* crow = (float*)g.C + row * g.ldc + n0 + wn * S::WN + (lane >> 5) * 4;
+    float mx = -INFINITY;
+    if (g.alpha != 1.f) {
+#pragma unroll
+      for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[i][j][e] *= g.alpha;
+    }
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) mx = fmaxf(mx, acc[i][j][e]);
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        *reinterpret_cast<float4*>(crow + j * 32 + q * 8) =
+            make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float sm = 0.f;
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) sm += __expf(acc[i][j][e] - mx);
+    sm += __shfl_xor(sm, 32, 64);
+    if (lane < 32) *reinterpret_cast<float2*>(g.rowstat + (row * nst + n0 / 64 + wn) * 2) = make_float2(mx, sm);
+  }
+}
+
 template <int BM, int BN, int WGM, int NWM, int NWD, int NWL, bool TRANS, bool C_BF16, int ST, int TAG, bool FULL, bool GEN,
-          bool Q4, bool PERS = false>
+          bool Q4, bool PERS = false, bool STAT = false>
 __global__ __launch_bounds__(64 * (NWM + NWD + NWL), 1) void gemm_q8f_kernel(Args g) {
   using S = Shape<BM, BN, WGM, NWM>;  // the MFMA waves' layout (epilogue included)
   constexpr int MB = S::MB, NB = S::NB, NT = 64 * (NWM + NWD + NWL);
@@ -341,7 +385,12 @@ __global__ __launch_bounds__(64 * (NWM + NWD + NWL), 1) void gemm_q8f_kernel(Arg
 #pragma unroll
       for (int i = 0; i < MB; i++)
 #pragma unroll
-        for (int j = 0; j < NB; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[q][i], fb[q][j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < NB; j++) {
+          // STAT: the transposed block (lane = one row of C, its 16 values along N), so a row's
+          // softmax statistics are lane-local
+          if constexpr (STAT) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[q][j], fa[q][i], acc[i][j], 0, 0, 0);
+          else acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[q][i], fb[q][j], acc[i][j], 0, 0, 0);
+        }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -426,7 +475,8 @@ __global__ __launch_bounds__(64 * (NWM + NWD + NWL), 1) void gemm_q8f_kernel(Arg
         if (u % sp == sp - 1) {
           int em0, en0;
           tile_origin(wg + (u / sp) * G, em0, en0);
-          gemm_epilogue<S, C_BF16, FULL>(g, acc, em0, en0, 0);
+          if constexpr (STAT) stat_epilogue<S>(g, acc, em0, en0);
+          else gemm_epilogue<S, C_BF16, FULL>(g, acc, em0, en0, 0);
 #pragma unroll
           for (int i = 0; i < MB; i++)
 #pragma unroll
@@ -529,6 +579,9 @@ static void launch_q8f_t(const Args& a, int c_bf16, int splits, hipStream_t s) {
   if (a.K2 > 0 && !a.ext_vec) {  // element-wise extension staging, general epilogue
     if (cb) launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, true, ST, TAG, false, true, Q4>, grid, block, s, a);
     else launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, false, ST, TAG, false, true, Q4>, grid, block, s, a);
+  } else if (a.rowstat) {  // the caller checked the conditions of the persistent form, fp32 C
+    const dim3 pgrid(num_cus() / 8 * 8);
+    launch_main(gemm_q8f_kernel<BM, BN, WGM, NWM, NWD, NWL, TRANS, false, ST, TAG, true, false, Q4, true, true>, pgrid, block, s, a);
   } else if (full && a.K2 <= BK && splits == 1 && !a.partial && a.tiles_m * a.tiles_n >= 4 * num_cus()) {
     // many tiles per CU: the persistent form, one workgroup per CU
     const dim3 pgrid(num_cus() / 8 * 8);

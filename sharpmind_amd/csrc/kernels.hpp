@@ -26,6 +26,10 @@ int ce_softmax_grad(const float* logits, const int32_t* labels, float* dL, float
                     int ignoreId, float smoothing, hipStream_t s);
 int ce_softmax_grad_bf16(const float* logits, const int32_t* labels, uint16_t* dL, float* loss,
                          int T, int V, int ignoreId, float smoothing, hipStream_t s);
+// the same with the row statistics precomputed by the logits' GEMM ([T][nst] (max, sum exp)
+// pairs over consecutive column blocks): the logits are read once; no label smoothing
+int ce_softmax_grad_bf16_stats(const float* logits, const float* stats, int nst, const int32_t* labels, uint16_t* dL,
+                               float* loss, int T, int V, int ignoreId, hipStream_t s);
 int adamw_update(float* data, const float* grad, float* m, float* v, int64_t n, float b1, float b2,
                  float bc1, float bc2, float lr, float eps, float decay, hipStream_t s);
 int l2normsq(const float* x, int64_t n, float* out, int accumulate, hipStream_t s);
