@@ -15,9 +15,10 @@
 // (buffer_load ... lds, two stages in flight, two workgroups per CU), and multiplies it
 // with v_mfma_f32_16x16x32_bf16 (16-column blocks: ranks 16/32/48 waste no MFMA columns).
 // Operands whose contiguous axis is m (or r) rather than k are DMA'd in their raw layout
-// (k rows) and transposed by the fragment reads (eight 16-bit LDS reads per fragment); the
-// raw Big rows are kept in 1 KiB blocks padded by 32 bytes so those column reads hit
-// distinct banks.  k-contiguous tiles use the XOR-swizzled [row][64] layout of the GEMM.
+// (k rows) and transposed by the fragment reads: Big with two ds_read_b64_tr_b16 per fragment
+// (its 16-byte m-chunks XOR-swizzled by k-row so that four consecutive k-rows hit distinct
+// banks), Small with eight 16-bit LDS reads; the raw Big rows are kept in 1 KiB blocks padded
+// by 32 bytes.  k-contiguous tiles use the XOR-swizzled [row][64] layout of the GEMM.
 // The reduction over K is split S ways (S chosen so the fp32 partials stay a small fraction
 // of the bytes of Big); a second kernel sums the S partials in a fixed order, so results are
 // deterministic and independent of timing.
@@ -79,6 +80,9 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("" ::: "memory");
 }
 
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_s4;
+
 // Big tile loader.  BIGK: k-contiguous rows m (swizzled [128][64]); else raw k-rows.
 // Each wave issues exactly 4 DMA instructions per stage.
 template <bool BIGK>
@@ -96,8 +100,10 @@ struct BigLoad {
         const int r = blk * 8 + (l >> 3), c = (l & 7) ^ ((r >> 1) & 7);
         off[j] = m0 + r < a.M ? (uint32_t)(((int64_t)(m0 + r) * a.ldb) * 2 + c * 16) : OOB;
       } else {
+        // raw k-rows, 16-byte m-chunks XOR-swizzled by 2 * (k-row % 4): the transposed fragment
+        // reads of four consecutive k-rows then hit distinct banks
         const int kr = blk * 4 + (l >> 4);
-        off[j] = (uint32_t)(((int64_t)kr * a.ldb + m0 + (l & 15) * 8) * 2);
+        off[j] = (uint32_t)(((int64_t)kr * a.ldb + m0 + ((l & 15) ^ (2 * (l >> 4))) * 8) * 2);
       }
     }
     kstep = BIGK ? BKT * 2 : (uint32_t)(BKT * a.ldb * 2);
@@ -117,14 +123,20 @@ struct BigLoad {
     if constexpr (BIGK) {
       return *reinterpret_cast<const bf16x8*>(stage + sw(row, kk * 4 + (l >> 4)));
     } else {
-      const int k0 = kk * 32 + 8 * (l >> 4);
-      bf16x8 v;
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const int k = k0 + j;
-        v[j] = *reinterpret_cast<const __bf16*>(stage + (k >> 2) * RAW_BLK + (k & 3) * 256 + row * 2);
-      }
-      return v;
+      // two ds_read_b64_tr_b16 over the 16 lanes of a k-group: source lane s reads 4 m of k-row
+      // k0 + 4h + s/4 at m = mb + 4 (s%4); destination lane s receives m = mb + s of those rows
+      const int s = l & 15, k0 = kk * 32 + 8 * (l >> 4), mb = row & ~15;
+      const int slot = ((mb + 4 * (s & 3)) >> 3) ^ (2 * (s >> 2));
+      const uint8_t* p = stage + (k0 >> 2) * RAW_BLK + (s >> 2) * 256 + slot * 16 + (s & 1) * 8;
+      short4v lo, hi;
+#if defined(__HIP_DEVICE_COMPILE__)
+      lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)p);
+      hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p + RAW_BLK));
+#else
+      lo = hi = short4v{};
+#endif
+      const uint2 x = __builtin_bit_cast(uint2, lo), y = __builtin_bit_cast(uint2, hi);
+      return __builtin_bit_cast(bf16x8, make_uint4(x.x, x.y, y.x, y.y));
     }
   }
 };
@@ -388,8 +400,6 @@ __global__ __launch_bounds__(256) void skinny_reduce_batch_kernel(BatchArgs b) {
 // (SMALLK) or, when it is [K][n] row-major, staged whole into LDS (K n 2 <= RS_SMALL bytes) and
 // read with ds_read_b64_tr_b16, which hands each lane four k-rows of its column.
 constexpr int RS_SMALL = 96 * 1024;
-typedef short short4v __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) short4v lds_s4;
 
 template <int NB, bool SMALLK>
 __device__ __forceinline__ bf16x8 rows_small_frag(const Args& a, const uint8_t* sm, int j, int k0, int lane) {
