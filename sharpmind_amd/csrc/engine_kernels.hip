@@ -165,9 +165,10 @@ __global__ void colsum_add2_kernel(const float* __restrict__ part, float* __rest
 
 // ---------------------------------------------------------------- vectorised form, D = 64 / 128
 // Half a wave (32 lanes) per (token, head) row, E = D/32 consecutive elements per lane, two
-// rows per wave.  NeoX rotation partners (d, d + D/2) sit 16 lanes apart in the same half
-// (__shfl_xor 16); adjacent pairs (2p, 2p+1) sit in one lane.  Same arithmetic per element
-// as the generic kernels above; the sum of squares / dot products reduce in a different order.
+// rows per wave.  Lane l holds elements (l % 2) D/2 + E (l / 2) ..: NeoX rotation partners
+// (d, d + D/2) sit in lanes l and l ^ 1 (one DPP move, no LDS round trip); adjacent pairs
+// (2p, 2p+1) sit in one lane.  Same arithmetic per element as the generic kernels above; the
+// sum of squares / dot products reduce in a different order.
 template <int E> struct VecF;
 template <> struct VecF<2> { typedef float2 T; };
 template <> struct VecF<4> { typedef float4 T; };
@@ -208,9 +209,18 @@ template <int E, typename TA> __device__ __forceinline__ void stE(TA* p, const f
     else *reinterpret_cast<uint32_t*>(p) = w[0];
   }
 }
+// lane l ^ 1's value (DPP quad permute, no LDS round trip)
+__device__ __forceinline__ float dpp_xor1(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+}
+// sum over the 32 lanes of a half wave: quad permutes (xor 1, xor 2), the 8- and 16-lane mirrors
+// by DPP, one cross-row shuffle; every lane ends with the same bits
 __device__ __forceinline__ float half_sum(float v) {
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  v += dpp_xor1(v);
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, true));
+  v += __shfl_xor(v, 16, 64);
   return v;
 }
 
@@ -222,6 +232,9 @@ __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
     int qk_norm, int neox, float eps) {
   constexpr int E = D / 32, P = D / 2, R = 4;  // R rows in flight per half-wave
   const int l = threadIdx.x & 31, hw = threadIdx.x >> 5;
+  // lane l holds elements eo .. eo + E - 1 of a head row, the halves interleaved so that NeoX
+  // partners (i, i + D/2) sit in lanes l and l ^ 1
+  const int eo = (l & 1) * P + E * (l >> 1);
   const int H = Hq + 2 * Hkv, nqkv = H * D;
   // workgroup per token: the half-waves take heads hw, hw + 8, ...; the lane's RoPE factors
   // depend only on the lane and the position, so they are loaded once per token
@@ -229,12 +242,12 @@ __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
     const int pos = t % S;
     float cs[E], sn[E];
     if (neox) {
-      ldE<E>(cosT + (int64_t)pos * P + (l * E) % P, cs);
-      ldE<E>(sinT + (int64_t)pos * P + (l * E) % P, sn);
+      ldE<E>(cosT + (int64_t)pos * P + eo % P, cs);
+      ldE<E>(sinT + (int64_t)pos * P + eo % P, sn);
     } else {
 #pragma unroll
       for (int i = 0; i < E; i += 2) {
-        const int p = (l * E + i) / 2;
+        const int p = (eo + i) / 2;
         cs[i] = cs[i + 1] = cosT[(int64_t)pos * P + p];
         sn[i] = sn[i + 1] = sinT[(int64_t)pos * P + p];
       }
@@ -244,17 +257,17 @@ __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
       float v[R][E];
 #pragma unroll
       for (int r = 0; r < R; r++)
-        if (h0 + 8 * r < H) ldE<E>(xt + (h0 + 8 * r) * D + l * E, v[r]);
+        if (h0 + 8 * r < H) ldE<E>(xt + (h0 + 8 * r) * D + eo, v[r]);
 #pragma unroll
       for (int r = 0; r < R; r++) {
         const int hh = h0 + 8 * r;
         if (hh >= H) break;
         if (hh >= Hq + Hkv) {
-          stE<E>(vo + (int64_t)t * Hkv * D + (hh - Hq - Hkv) * D + l * E, v[r]);
+          stE<E>(vo + (int64_t)t * Hkv * D + (hh - Hq - Hkv) * D + eo, v[r]);
           continue;
         }
         const bool isq = hh < Hq;
-        const float* w = (isq ? wq : wk) + l * E;
+        const float* w = (isq ? wq : wk) + eo;
         if (qk_norm) {
           float ss = 0.f;
 #pragma unroll
@@ -267,10 +280,10 @@ __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
         }
         float o[E];
         if (neox) {
-          const bool lo = l * E < P;
+          const bool lo = eo < P;
 #pragma unroll
           for (int i = 0; i < E; i++) {
-            const float partner = __shfl_xor(v[r][i], 16, 64);
+            const float partner = dpp_xor1(v[r][i]);
             o[i] = lo ? v[r][i] * cs[i] - partner * sn[i] : v[r][i] * cs[i] + partner * sn[i];
           }
         } else {
@@ -280,7 +293,7 @@ __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
             o[i + 1] = v[r][i + 1] * cs[i] + v[r][i] * sn[i];
           }
         }
-        stE<E>((isq ? qo + (int64_t)t * Hq * D + hh * D : ko + (int64_t)t * Hkv * D + (hh - Hq) * D) + l * E, o);
+        stE<E>((isq ? qo + (int64_t)t * Hq * D + hh * D : ko + (int64_t)t * Hkv * D + (hh - Hq) * D) + eo, o);
       }
     }
   }
@@ -295,14 +308,15 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
     int kv_grp) {
   constexpr int E = D / 32, P = D / 2;
   const int l = threadIdx.x & 31, hw = threadIdx.x >> 5;  // half-wave 0..7
+  const int eo = (l & 1) * P + E * (l >> 1);  // as in the forward: NeoX partners in lanes l, l ^ 1
   // kv_grp > 0: dk / dv are the attention backward's per-query-head partials [T, Hq, D]; a KV
   // head's gradient is the sum of its kv_grp query heads, added in ascending head order
   auto ld_kv = [&](const TG* base, int t, int kvh, float* g) {
     if (kv_grp == 0) {
-      ldE<E>(base + (int64_t)t * Hkv * D + kvh * D + l * E, g);
+      ldE<E>(base + (int64_t)t * Hkv * D + kvh * D + eo, g);
       return;
     }
-    const TG* p0 = base + ((int64_t)t * Hq + (int64_t)kvh * kv_grp) * D + l * E;
+    const TG* p0 = base + ((int64_t)t * Hq + (int64_t)kvh * kv_grp) * D + eo;
     float h[E];
 #pragma unroll
     for (int i = 0; i < E; i++) g[i] = 0.f;
@@ -330,12 +344,12 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
     const int pos = t % S;
     float cs[E], sn[E];
     if (neox) {
-      ldE<E>(cosT + (int64_t)pos * P + (l * E) % P, cs);
-      ldE<E>(sinT + (int64_t)pos * P + (l * E) % P, sn);
+      ldE<E>(cosT + (int64_t)pos * P + eo % P, cs);
+      ldE<E>(sinT + (int64_t)pos * P + eo % P, sn);
     } else {
 #pragma unroll
       for (int i = 0; i < E; i += 2) {
-        const int p = (l * E + i) / 2;
+        const int p = (eo + i) / 2;
         cs[i] = cs[i + 1] = cosT[(int64_t)pos * P + p];
         sn[i] = sn[i + 1] = sinT[(int64_t)pos * P + p];
       }
@@ -350,10 +364,10 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
           ld_kv(dv, t, hh - Hq - Hkv, g[r]);
           continue;
         }
-        if (hh < Hq) ldE<E>(dq + (int64_t)t * Hq * D + hh * D + l * E, g[r]);
+        if (hh < Hq) ldE<E>(dq + (int64_t)t * Hq * D + hh * D + eo, g[r]);
         else ld_kv(dk, t, hh - Hq, g[r]);
         if (qk_norm) {
-          ldE<E>(qkv + (int64_t)t * nqkv + hh * D + l * E, x[r]);
+          ldE<E>(qkv + (int64_t)t * nqkv + hh * D + eo, x[r]);
           ri[r] = rinv[(int64_t)t * (Hq + Hkv) + hh];
         }
       }
@@ -361,7 +375,7 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
       for (int r = 0; r < R; r++) {
         const int hh = h0 + 8 * r;
         if (hh >= H) break;
-        TA* dst = dqkv + (int64_t)t * nqkv + hh * D + l * E;
+        TA* dst = dqkv + (int64_t)t * nqkv + hh * D + eo;
         if (hh >= Hq + Hkv) {
           stE<E>(dst, g[r]);
           continue;
@@ -369,10 +383,10 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
         const bool isq = hh < Hq;
         float gr[E];
         if (neox) {
-          const bool lo = l * E < P;
+          const bool lo = eo < P;
 #pragma unroll
           for (int i = 0; i < E; i++) {
-            const float partner = __shfl_xor(g[r][i], 16, 64);
+            const float partner = dpp_xor1(g[r][i]);
             gr[i] = lo ? cs[i] * g[r][i] + sn[i] * partner : -sn[i] * partner + cs[i] * g[r][i];
           }
         } else {
@@ -386,7 +400,7 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
           stE<E>(dst, gr);
           continue;
         }
-        const float* w = (isq ? wq : wk) + l * E;
+        const float* w = (isq ? wq : wk) + eo;
         float dot = 0.f, xn[E];
 #pragma unroll
         for (int i = 0; i < E; i++) {
@@ -407,8 +421,8 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
     __shared__ float sh[8][2][D];
 #pragma unroll
     for (int i = 0; i < E; i++) {
-      sh[hw][0][l * E + i] = aq[i];
-      sh[hw][1][l * E + i] = ak[i];
+      sh[hw][0][eo + i] = aq[i];
+      sh[hw][1][eo + i] = ak[i];
     }
     __syncthreads();
     for (int c = threadIdx.x; c < 2 * D; c += 256) {
