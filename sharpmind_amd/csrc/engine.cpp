@@ -450,14 +450,15 @@ static Operand lora_op(const Engine* e, const DenseRef& t, bool kmode, int64_t l
 }
 
 // y (fp32 or TA) = x W^T [+ s (x A) B] [+ bias] [+ R]
-static int proj_forward(Engine* e, int l, int p, const void* x, void* y, int y_bf16, const float* R, hipStream_t s) {
+static int proj_forward(Engine* e, int l, int p, const void* x, void* y, int y_bf16, const float* R, hipStream_t s,
+                        bool u_ready = false) {
   LayerW& w = e->L[l];
   const int T = e->T, In = e->In[p], Out = e->Out[p];
   GemmArgs g{};
   g.precision = prec(e);
   g.alpha = 1.f;
   g.split_k = 1;
-  if (e->lora) {  // u = x A  (saved for dB)
+  if (e->lora) {  // u = x A  (saved for dB; u_ready: the RMSNorm producing x computed it)
     const int nr = e->nr[p];
     GemmArgs u{};
     u.precision = prec(e);
@@ -467,7 +468,8 @@ static int proj_forward(Engine* e, int l, int p, const void* x, void* y, int y_b
     u.B = lora_op(e, w.la[p], false, nr);
     u.C = e->sv[l].u[p]; u.ldc = nr; u.c_bf16 = e->bf;
     u.split_k = split_arg(e, T, nr, In);
-    if (int rc = gemm(u, s)) return rc;
+    if (!u_ready)
+      if (int rc = gemm(u, s)) return rc;
     g.K2 = nr;
     g.A2 = act_k(e, e->sv[l].u[p], nr);
     g.B2 = lora_op(e, w.lb[p], false, Out);
@@ -585,9 +587,17 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
     Saved& sv = e->sv[l];
     LayerW& w = e->L[l];
     float* h_out = (l + 1 < c.n_layers) ? e->sv[l + 1].h_in : e->h_fin;
-    R_(rmsnorm_forward(sv.h_in, w.norm1.data, e->bf ? nullptr : (float*)sv.xn1, e->bf ? (uint16_t*)sv.xn1 : nullptr,
-                       sv.rinv1, T, d, c.norm_eps, s));
-    R_(proj_forward(e, l, P_QKV, sv.xn1, sv.qkv, e->qkv_bf, nullptr, s));
+    // bf16 LoRA: the RMSNorm also computes the qkv adapters' u = xn A (rows already in registers)
+    int fused = 0;
+    if (e->lora && e->bf && w.la[P_QKV].bf) {
+      fused = rmsnorm_lora_u(sv.h_in, w.norm1.data, c.norm_eps, (uint16_t*)sv.xn1, sv.rinv1, (const uint16_t*)w.la[P_QKV].bf,
+                             e->nr[P_QKV], (uint16_t*)sv.u[P_QKV], T, d, s);
+      if (fused < 0) return fused;
+    }
+    if (!fused)
+      R_(rmsnorm_forward(sv.h_in, w.norm1.data, e->bf ? nullptr : (float*)sv.xn1, e->bf ? (uint16_t*)sv.xn1 : nullptr,
+                         sv.rinv1, T, d, c.norm_eps, s));
+    R_(proj_forward(e, l, P_QKV, sv.xn1, sv.qkv, e->qkv_bf, nullptr, s, fused == 1));
     R_(qkv_prep_forward(sv.qkv, e->qkv_bf, sv.q, sv.k, sv.v, sv.rinv_qk, c.qk_norm ? w.qn.data : nullptr,
                         c.qk_norm ? w.kn.data : nullptr, e->cosT, e->sinT, T, c.seq, Hq, Hkv, D, c.qk_norm,
                         c.rope_neox, c.norm_eps, e->bf, s));
@@ -599,9 +609,16 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
                                  c.batch, c.seq, Hq, Hkv, D, s));
     }
     R_(proj_forward(e, l, P_O, sv.o, sv.h_mid, 0, sv.h_in, s));  // h_mid = h_in + attn
-    R_(rmsnorm_forward(sv.h_mid, w.norm2.data, e->bf ? nullptr : (float*)sv.xn2, e->bf ? (uint16_t*)sv.xn2 : nullptr,
-                       sv.rinv2, T, d, c.norm_eps, s));
-    R_(proj_forward(e, l, P_GU, sv.xn2, sv.gu, e->bf, nullptr, s));
+    fused = 0;
+    if (e->lora && e->bf && w.la[P_GU].bf) {
+      fused = rmsnorm_lora_u(sv.h_mid, w.norm2.data, c.norm_eps, (uint16_t*)sv.xn2, sv.rinv2, (const uint16_t*)w.la[P_GU].bf,
+                             e->nr[P_GU], (uint16_t*)sv.u[P_GU], T, d, s);
+      if (fused < 0) return fused;
+    }
+    if (!fused)
+      R_(rmsnorm_forward(sv.h_mid, w.norm2.data, e->bf ? nullptr : (float*)sv.xn2, e->bf ? (uint16_t*)sv.xn2 : nullptr,
+                         sv.rinv2, T, d, c.norm_eps, s));
+    R_(proj_forward(e, l, P_GU, sv.xn2, sv.gu, e->bf, nullptr, s, fused == 1));
     R_(swiglu_fused_forward(sv.gu, sv.act, T, F, e->bf, s));
     R_(proj_forward(e, l, P_D, sv.act, h_out, 0, sv.h_mid, s));  // h_out = h_mid + ffn
   }

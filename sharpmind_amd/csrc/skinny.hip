@@ -504,6 +504,95 @@ __global__ __launch_bounds__(64 * NW) void skinny_rows_kernel(Args a) {
   }
 }
 
+// RMSNorm forward fused with the LoRA down-projection of its output (the producer of x computes
+// u = x A while the rows are in registers): xn = h * rinv * w (bf16 out), rinv = 1/sqrt(mean h^2 +
+// eps), u[t, :] = xn[t, :] A (A [D][n] bf16, n = 16 NB), bf16 out.  Workgroup = 16 rows and 8
+// waves; wave w takes K columns [w D/8, (w+1) D/8) in 32-wide slices, each lane 8 consecutive
+// columns of one row per slice -- the layout of the MFMA A fragment, so the normalised bf16 values
+// feed v_mfma_f32_16x16x32_bf16 directly.  The row's sum of squares is summed over the four lanes
+// of a row (xor 16, 32) and then over the waves in order; A is staged in LDS and read transposed
+// as in the row-block product.
+template <int NB, int NS>  // NS = 32-wide slices per wave (D / 256)
+__global__ __launch_bounds__(512) void rmsnorm_lora_u_kernel(const float* __restrict__ h, const float* __restrict__ wn,
+                                                            float eps, uint16_t* __restrict__ xn, float* __restrict__ rinv,
+                                                            Args a) {
+  constexpr int NW = 8;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[RS_SMALL + NW * NB * 64 * 16];
+  __shared__ float ssq[NW][16];
+  __shared__ float sri[16];
+  uint8_t* red = smem + RS_SMALL;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, rl = lane & 15;
+  const int D = a.K, m0 = blockIdx.x * 16, row = min(m0 + rl, a.M - 1);
+  const int kb = w * (D / NW);
+  const float* hr = h + (int64_t)row * D + kb + 8 * g;
+  float v[NS][8];
+#pragma unroll
+  for (int t = 0; t < NS; t++) {
+    const float4 x0 = *reinterpret_cast<const float4*>(hr + 32 * t);
+    const float4 x1 = *reinterpret_cast<const float4*>(hr + 32 * t + 4);
+    v[t][0] = x0.x; v[t][1] = x0.y; v[t][2] = x0.z; v[t][3] = x0.w;
+    v[t][4] = x1.x; v[t][5] = x1.y; v[t][6] = x1.z; v[t][7] = x1.w;
+  }
+  {  // stage A [D][n] while h is in flight
+    const int nv = D * a.n / 8;
+    for (int i = threadIdx.x; i < nv; i += 64 * NW)
+      reinterpret_cast<uint4*>(smem)[i] = reinterpret_cast<const uint4*>(a.small)[i];
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < NS; t++)
+#pragma unroll
+    for (int i = 0; i < 8; i++) ss += v[t][i] * v[t][i];
+  ss += __shfl_xor(ss, 16, 64);
+  ss += __shfl_xor(ss, 32, 64);
+  if (g == 0) ssq[w][rl] = ss;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    float tot = 0.f;
+    for (int q = 0; q < NW; q++) tot += ssq[q][threadIdx.x];
+    const float ri = 1.f / sqrtf(tot / (float)D + eps);
+    sri[threadIdx.x] = ri;
+    if (m0 + (int)threadIdx.x < a.M) rinv[m0 + threadIdx.x] = ri;
+  }
+  __syncthreads();
+  const float ri = sri[rl];
+  floatx4 acc[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < NS; t++) {
+    const int k0 = kb + 32 * t;
+    const float4 w0 = *reinterpret_cast<const float4*>(wn + k0 + 8 * g);
+    const float4 w1 = *reinterpret_cast<const float4*>(wn + k0 + 8 * g + 4);
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    uint32_t pk[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) pk[i] = pack_bf2(v[t][2 * i] * ri * wv[2 * i], v[t][2 * i + 1] * ri * wv[2 * i + 1]);
+    const uint4 u4 = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    if (m0 + rl < a.M) *reinterpret_cast<uint4*>(xn + (int64_t)(m0 + rl) * D + k0 + 8 * g) = u4;
+    const bf16x8 fa = __builtin_bit_cast(bf16x8, u4);
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, rows_small_frag<NB, false>(a, smem, j, k0, lane), acc[j], 0, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < NB; j++) *reinterpret_cast<floatx4*>(red + ((w * NB + j) * 64 + lane) * 16) = acc[j];
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    floatx4 o = *reinterpret_cast<const floatx4*>(red + (j * 64 + lane) * 16);
+#pragma unroll
+    for (int q = 1; q < NW; q++) o += *reinterpret_cast<const floatx4*>(red + ((q * NB + j) * 64 + lane) * 16);
+    const int col = 16 * j + (lane & 15);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int r = m0 + 4 * (lane >> 4) + e;
+      if (r < a.M) ((uint16_t*)a.C)[(int64_t)r * a.ldc + col] = f2bf(o[e]);
+    }
+  }
+}
+
 template <bool SMALLK, bool TRANS_OUT, bool C_BF16, int NW>
 static void launch_rows_nw(int nb, const Args& a, hipStream_t s) {
   const dim3 grid(ceil_div(a.M, 16)), block(64 * NW);
@@ -579,6 +668,39 @@ int skinny_release(SkinnyHold* h, hipStream_t s) {
   SMHIP_CHECK_LAUNCH();
   prof_add(PROF_GEMM, ev0, prof_mark(s), 2.0 * h->M * h->n * (double)h->K, h->M, h->n, h->K);
   return SMHIP_OK;
+}
+
+// Returns 1 when the fused kernel ran, 0 when the shapes do not fit it (the caller runs the
+// RMSNorm and the rank product separately).
+int rmsnorm_lora_u(const float* h, const float* w, float eps, uint16_t* xn, float* rinv, const uint16_t* A, int n,
+                   uint16_t* u, int T, int D, hipStream_t s) {
+  using namespace sk;
+  if (T <= 0) return 1;
+  if (D % 256 || D > 2048 || n % 16 || n < 16 || n > 64 || (int64_t)D * n * 2 > RS_SMALL) return 0;
+  if (((uintptr_t)h | (uintptr_t)w | (uintptr_t)xn | (uintptr_t)A) % 16) return 0;
+  Args a{};
+  a.small = A;
+  a.lds = n;
+  a.M = T; a.n = n; a.K = D;
+  a.C = u; a.ldc = n;
+  const dim3 grid(ceil_div(T, 16)), block(512);
+#define SMHIP_RLU(NB)                                                                                       \
+  switch (D / 256) {                                                                                        \
+    case 1: hipLaunchKernelGGL((rmsnorm_lora_u_kernel<NB, 1>), grid, block, 0, s, h, w, eps, xn, rinv, a); break; \
+    case 2: hipLaunchKernelGGL((rmsnorm_lora_u_kernel<NB, 2>), grid, block, 0, s, h, w, eps, xn, rinv, a); break; \
+    case 3: hipLaunchKernelGGL((rmsnorm_lora_u_kernel<NB, 3>), grid, block, 0, s, h, w, eps, xn, rinv, a); break; \
+    case 4: hipLaunchKernelGGL((rmsnorm_lora_u_kernel<NB, 4>), grid, block, 0, s, h, w, eps, xn, rinv, a); break; \
+    default: return 0;                                                                                      \
+  }
+  switch (n / 16) {
+    case 1: SMHIP_RLU(1) break;
+    case 2: SMHIP_RLU(2) break;
+    case 3: SMHIP_RLU(3) break;
+    default: SMHIP_RLU(4) break;
+  }
+#undef SMHIP_RLU
+  SMHIP_CHECK_LAUNCH();
+  return 1;
 }
 
 int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, const void* small, int64_t lds,
