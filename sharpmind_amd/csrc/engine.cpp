@@ -54,6 +54,7 @@ struct LayerW {
   uint16_t* wb[4] = {};      // LoRA bf16 mode with the base workspace: bf16 [Out][In] and [In][Out]
   uint16_t* wbt[4] = {};
   DenseRef la[4], lb[4];     // LoRA A [In, nr], B [nr, Out]
+  uint16_t* lat[4] = {};     // bf16 LoRA: A transposed, [nr][In] (k-contiguous operand of u = x A)
   int* lb_cols = nullptr;    // device: column start of each diagonal block
 };
 
@@ -93,6 +94,9 @@ struct Engine {
   DequantJob* dq_jobs = nullptr;  // device table of the per-step decode (one launch)
   int dq_njobs = 0;
   int64_t dq_tiles = 0;
+  BfTJob* lat_jobs = nullptr;  // device table of the per-step LoRA A transposes (one launch)
+  int lat_njobs = 0;
+  int64_t lat_max = 0;
   std::vector<LayerW> L;
   std::map<std::string, DenseRef*> dense_by_name;
   // activations
@@ -212,6 +216,29 @@ static int build(Engine* e) {
     it.ref->grad = nullptr;
     it.ref->n = it.n;
     off += it.n;
+  }
+  if (e->lora && e->bf) {  // transposed bf16 copies of the LoRA A shadows, refreshed each step
+    std::vector<BfTJob> jobs;
+    int64_t tot = 0;
+    for (int l = 0; l < c.n_layers; l++)
+      for (int p = 0; p < 4; p++) tot += (int64_t)e->In[p] * e->nr[p];
+    uint16_t* at = (uint16_t*)dalloc(e, sizeof(uint16_t) * (size_t)std::max<int64_t>(tot, 1));
+    if (!at) return fail(SMHIP_ENOMEM, "engine: transposed adapters");
+    for (int l = 0; l < c.n_layers; l++)
+      for (int p = 0; p < 4; p++) {
+        LayerW& w = e->L[l];
+        if (!w.la[p].bf) continue;
+        w.lat[p] = at;
+        jobs.push_back(BfTJob{w.la[p].bf, at, e->In[p], e->nr[p]});
+        e->lat_max = std::max<int64_t>(e->lat_max, (int64_t)e->In[p] * e->nr[p]);
+        at += (int64_t)e->In[p] * e->nr[p];
+      }
+    if (!jobs.empty()) {
+      e->lat_njobs = (int)jobs.size();
+      e->lat_jobs = (BfTJob*)dalloc(e, sizeof(BfTJob) * jobs.size());
+      if (!e->lat_jobs) return fail(SMHIP_ENOMEM, "engine: transpose table");
+      SMHIP_CHECK_HIP(hipMemcpy(e->lat_jobs, jobs.data(), sizeof(BfTJob) * jobs.size(), hipMemcpyHostToDevice));
+    }
   }
 
   // --- LoRA: quantised base planes and block-diagonal column starts
@@ -465,7 +492,7 @@ static int proj_forward(Engine* e, int l, int p, const void* x, void* y, int y_b
     u.alpha = 1.f;
     u.M = T; u.N = nr; u.K = In;
     u.A = act_k(e, x, In);
-    u.B = lora_op(e, w.la[p], false, nr);
+    u.B = w.lat[p] ? Operand{SRC_BF16_K, w.lat[p], nullptr, In} : lora_op(e, w.la[p], false, nr);
     u.C = e->sv[l].u[p]; u.ldc = nr; u.c_bf16 = e->bf;
     u.split_k = split_arg(e, T, nr, In);
     if (!u_ready)
@@ -574,6 +601,8 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
 
   // decode the frozen base into the bf16 workspace (both layouts), all matrices in one launch
   if (e->base_ws) R_(dequant_bf16_many(e->dq_jobs, e->dq_njobs, e->dq_tiles, s));
+  // the adapters' A shadows (rewritten by every optimizer step and parameter load) transposed
+  if (e->lat_jobs) R_(transpose_bf16_jobs(e->lat_jobs, e->lat_njobs, e->lat_max, s));
 
   // ---------------- forward
   if (e->lora) {
@@ -589,8 +618,8 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
     float* h_out = (l + 1 < c.n_layers) ? e->sv[l + 1].h_in : e->h_fin;
     // bf16 LoRA: the RMSNorm also computes the qkv adapters' u = xn A (rows already in registers)
     int fused = 0;
-    if (e->lora && e->bf && w.la[P_QKV].bf) {
-      fused = rmsnorm_lora_u(sv.h_in, w.norm1.data, c.norm_eps, (uint16_t*)sv.xn1, sv.rinv1, (const uint16_t*)w.la[P_QKV].bf,
+    if (e->lora && e->bf && w.lat[P_QKV]) {
+      fused = rmsnorm_lora_u(sv.h_in, w.norm1.data, c.norm_eps, (uint16_t*)sv.xn1, sv.rinv1, w.lat[P_QKV],
                              e->nr[P_QKV], (uint16_t*)sv.u[P_QKV], T, d, s);
       if (fused < 0) return fused;
     }
@@ -610,8 +639,8 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
     }
     R_(proj_forward(e, l, P_O, sv.o, sv.h_mid, 0, sv.h_in, s));  // h_mid = h_in + attn
     fused = 0;
-    if (e->lora && e->bf && w.la[P_GU].bf) {
-      fused = rmsnorm_lora_u(sv.h_mid, w.norm2.data, c.norm_eps, (uint16_t*)sv.xn2, sv.rinv2, (const uint16_t*)w.la[P_GU].bf,
+    if (e->lora && e->bf && w.lat[P_GU]) {
+      fused = rmsnorm_lora_u(sv.h_mid, w.norm2.data, c.norm_eps, (uint16_t*)sv.xn2, sv.rinv2, w.lat[P_GU],
                              e->nr[P_GU], (uint16_t*)sv.u[P_GU], T, d, s);
       if (fused < 0) return fused;
     }

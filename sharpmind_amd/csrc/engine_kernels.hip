@@ -816,4 +816,24 @@ int zero_bytes(void* p, size_t bytes, hipStream_t s) {
   SMHIP_CHECK_LAUNCH();
   return SMHIP_OK;
 }
+// ---------------------------------------------------------------- batched bf16 transposes
+// grid (element blocks, jobs): destination-ordered (coalesced stores), the small source rows
+// gathered
+__global__ __launch_bounds__(256) void transpose_bf16_jobs_kernel(const BfTJob* __restrict__ jobs) {
+  const BfTJob j = jobs[blockIdx.y];
+  const int64_t n = (int64_t)j.rows * j.cols;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t c = i / j.rows, r = i - c * j.rows;
+    j.dst[i] = j.src[r * j.cols + c];
+  }
+}
+
+int transpose_bf16_jobs(const BfTJob* jobs_dev, int njobs, int64_t max_elems, hipStream_t s) {
+  if (njobs <= 0) return SMHIP_OK;
+  const int gx = (int)std::min<int64_t>((max_elems + 255) / 256, 64);
+  hipLaunchKernelGGL(transpose_bf16_jobs_kernel, dim3(gx, njobs), dim3(256), 0, s, jobs_dev);
+  SMHIP_CHECK_LAUNCH();
+  return SMHIP_OK;
+}
+
 }  // namespace smhip

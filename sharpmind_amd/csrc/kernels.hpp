@@ -80,9 +80,16 @@ struct SkinnyHold {
   unsigned char args[256];  // the product's kernel arguments (sk::Args)
 };
 int skinny_release(SkinnyHold* h, hipStream_t s);
-// RMSNorm forward (bf16 output) fused with u = xn A for a LoRA A [D][n] (bf16); 1 = done, 0 = shape
+// batched bf16 transposes: dst [cols][rows] = src [rows][cols] for each job (one launch)
+struct BfTJob {
+  const uint16_t* src;
+  uint16_t* dst;
+  int rows, cols;
+};
+int transpose_bf16_jobs(const BfTJob* jobs_dev, int njobs, int64_t max_elems, hipStream_t s);
+// RMSNorm forward (bf16 output) fused with u = xn A for a LoRA A given transposed, At [n][D] (bf16); 1 = done, 0 = shape
 // not supported (run rmsnorm_forward and the rank product instead)
-int rmsnorm_lora_u(const float* h, const float* w, float eps, uint16_t* xn, float* rinv, const uint16_t* A, int n,
+int rmsnorm_lora_u(const float* h, const float* w, float eps, uint16_t* xn, float* rinv, const uint16_t* At, int n,
                    uint16_t* u, int T, int D, hipStream_t s);
 int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, const void* small, int64_t lds,
                 bool small_k, float alpha, float beta, void* C, int64_t ldc, bool trans_out, bool c_bf16,

@@ -506,23 +506,25 @@ __global__ __launch_bounds__(64 * NW) void skinny_rows_kernel(Args a) {
 
 // RMSNorm forward fused with the LoRA down-projection of its output (the producer of x computes
 // u = x A while the rows are in registers): xn = h * rinv * w (bf16 out), rinv = 1/sqrt(mean h^2 +
-// eps), u[t, :] = xn[t, :] A (A [D][n] bf16, n = 16 NB), bf16 out.  Workgroup = 16 rows and 8
-// waves; wave w takes K columns [w D/8, (w+1) D/8) in 32-wide slices, each lane 8 consecutive
-// columns of one row per slice -- the layout of the MFMA A fragment, so the normalised bf16 values
-// feed v_mfma_f32_16x16x32_bf16 directly.  The row's sum of squares is summed over the four lanes
-// of a row (xor 16, 32) and then over the waves in order; A is staged in LDS and read transposed
-// as in the row-block product.
+// eps), u[t, :] = xn[t, :] A, bf16 out, with A given transposed (At [n][D] bf16, n = 16 NB).
+// Workgroup = 16 rows and 8 waves; wave w takes K columns [w D/8, (w+1) D/8) in 32-wide slices,
+// each lane 8 consecutive columns of one row per slice -- the layout of the MFMA A fragment, so
+// the normalised bf16 values feed v_mfma_f32_16x16x32_bf16 directly.  The B fragment of a lane
+// (column 16 j + lane % 16, 8 consecutive k) is one 16-byte load of an At row, issued before the
+// row statistics so it is in flight behind them; At (n D 2 bytes) stays in L2 across workgroups.
+// The row's sum of squares is summed over the four lanes of a row (xor 16, 32), then over the
+// waves in order.
 template <int NB, int NS>  // NS = 32-wide slices per wave (D / 256)
 __global__ __launch_bounds__(512) void rmsnorm_lora_u_kernel(const float* __restrict__ h, const float* __restrict__ wn,
                                                             float eps, uint16_t* __restrict__ xn, float* __restrict__ rinv,
-                                                            Args a) {
+                                                            const uint16_t* __restrict__ At, uint16_t* __restrict__ u,
+                                                            int M, int D, int n) {
   constexpr int NW = 8;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[RS_SMALL + NW * NB * 64 * 16];
+  __shared__ __attribute__((aligned(16))) uint8_t red[NW * NB * 64 * 16];
   __shared__ float ssq[NW][16];
   __shared__ float sri[16];
-  uint8_t* red = smem + RS_SMALL;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, rl = lane & 15;
-  const int D = a.K, m0 = blockIdx.x * 16, row = min(m0 + rl, a.M - 1);
+  const int m0 = blockIdx.x * 16, row = min(m0 + rl, M - 1);
   const int kb = w * (D / NW);
   const float* hr = h + (int64_t)row * D + kb + 8 * g;
   float v[NS][8];
@@ -533,11 +535,12 @@ __global__ __launch_bounds__(512) void rmsnorm_lora_u_kernel(const float* __rest
     v[t][0] = x0.x; v[t][1] = x0.y; v[t][2] = x0.z; v[t][3] = x0.w;
     v[t][4] = x1.x; v[t][5] = x1.y; v[t][6] = x1.z; v[t][7] = x1.w;
   }
-  {  // stage A [D][n] while h is in flight
-    const int nv = D * a.n / 8;
-    for (int i = threadIdx.x; i < nv; i += 64 * NW)
-      reinterpret_cast<uint4*>(smem)[i] = reinterpret_cast<const uint4*>(a.small)[i];
-  }
+  bf16x8 fb[NS][NB];
+#pragma unroll
+  for (int t = 0; t < NS; t++)
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+      fb[t][j] = *reinterpret_cast<const bf16x8*>(At + (int64_t)(16 * j + rl) * D + kb + 32 * t + 8 * g);
   float ss = 0.f;
 #pragma unroll
   for (int t = 0; t < NS; t++)
@@ -552,7 +555,7 @@ __global__ __launch_bounds__(512) void rmsnorm_lora_u_kernel(const float* __rest
     for (int q = 0; q < NW; q++) tot += ssq[q][threadIdx.x];
     const float ri = 1.f / sqrtf(tot / (float)D + eps);
     sri[threadIdx.x] = ri;
-    if (m0 + (int)threadIdx.x < a.M) rinv[m0 + threadIdx.x] = ri;
+    if (m0 + (int)threadIdx.x < M) rinv[m0 + threadIdx.x] = ri;
   }
   __syncthreads();
   const float ri = sri[rl];
@@ -569,11 +572,10 @@ __global__ __launch_bounds__(512) void rmsnorm_lora_u_kernel(const float* __rest
 #pragma unroll
     for (int i = 0; i < 4; i++) pk[i] = pack_bf2(v[t][2 * i] * ri * wv[2 * i], v[t][2 * i + 1] * ri * wv[2 * i + 1]);
     const uint4 u4 = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-    if (m0 + rl < a.M) *reinterpret_cast<uint4*>(xn + (int64_t)(m0 + rl) * D + k0 + 8 * g) = u4;
+    if (m0 + rl < M) *reinterpret_cast<uint4*>(xn + (int64_t)(m0 + rl) * D + k0 + 8 * g) = u4;
     const bf16x8 fa = __builtin_bit_cast(bf16x8, u4);
 #pragma unroll
-    for (int j = 0; j < NB; j++)
-      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, rows_small_frag<NB, false>(a, smem, j, k0, lane), acc[j], 0, 0, 0);
+    for (int j = 0; j < NB; j++) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, fb[t][j], acc[j], 0, 0, 0);
   }
 #pragma unroll
   for (int j = 0; j < NB; j++) *reinterpret_cast<floatx4*>(red + ((w * NB + j) * 64 + lane) * 16) = acc[j];
@@ -588,7 +590,7 @@ __global__ __launch_bounds__(512) void rmsnorm_lora_u_kernel(const float* __rest
 #pragma unroll
     for (int e = 0; e < 4; e++) {
       const int r = m0 + 4 * (lane >> 4) + e;
-      if (r < a.M) ((uint16_t*)a.C)[(int64_t)r * a.ldc + col] = f2bf(o[e]);
+      if (r < M) u[(int64_t)r * n + col] = f2bf(o[e]);
     }
   }
 }
@@ -671,26 +673,20 @@ int skinny_release(SkinnyHold* h, hipStream_t s) {
 }
 
 // Returns 1 when the fused kernel ran, 0 when the shapes do not fit it (the caller runs the
-// RMSNorm and the rank product separately).
-int rmsnorm_lora_u(const float* h, const float* w, float eps, uint16_t* xn, float* rinv, const uint16_t* A, int n,
+// RMSNorm and the rank product separately).  At is A transposed, [n][D].
+int rmsnorm_lora_u(const float* h, const float* w, float eps, uint16_t* xn, float* rinv, const uint16_t* At, int n,
                    uint16_t* u, int T, int D, hipStream_t s) {
   using namespace sk;
   if (T <= 0) return 1;
-  if (D % 256 || D > 2048 || n % 16 || n < 16 || n > 64 || (int64_t)D * n * 2 > RS_SMALL) return 0;
-  if (((uintptr_t)h | (uintptr_t)w | (uintptr_t)xn | (uintptr_t)A) % 16) return 0;
-  Args a{};
-  a.small = A;
-  a.lds = n;
-  a.M = T; a.n = n; a.K = D;
-  a.C = u; a.ldc = n;
+  if (D % 256 || D > 1024 || n % 16 || n < 16 || n > 64) return 0;
+  if (((uintptr_t)h | (uintptr_t)w | (uintptr_t)xn | (uintptr_t)At) % 16) return 0;
   const dim3 grid(ceil_div(T, 16)), block(512);
 #define SMHIP_RLU(NB)                                                                                       \
   switch (D / 256) {                                                                                        \
-    case 1: hipLaunchKernelGGL((rmsnorm_lora_u_kernel<NB, 1>), grid, block, 0, s, h, w, eps, xn, rinv, a); break; \
-    case 2: hipLaunchKernelGGL((rmsnorm_lora_u_kernel<NB, 2>), grid, block, 0, s, h, w, eps, xn, rinv, a); break; \
-    case 3: hipLaunchKernelGGL((rmsnorm_lora_u_kernel<NB, 3>), grid, block, 0, s, h, w, eps, xn, rinv, a); break; \
-    case 4: hipLaunchKernelGGL((rmsnorm_lora_u_kernel<NB, 4>), grid, block, 0, s, h, w, eps, xn, rinv, a); break; \
-    default: return 0;                                                                                      \
+    case 1: hipLaunchKernelGGL((rmsnorm_lora_u_kernel<NB, 1>), grid, block, 0, s, h, w, eps, xn, rinv, At, u, T, D, n); break; \
+    case 2: hipLaunchKernelGGL((rmsnorm_lora_u_kernel<NB, 2>), grid, block, 0, s, h, w, eps, xn, rinv, At, u, T, D, n); break; \
+    case 3: hipLaunchKernelGGL((rmsnorm_lora_u_kernel<NB, 3>), grid, block, 0, s, h, w, eps, xn, rinv, At, u, T, D, n); break; \
+    default: hipLaunchKernelGGL((rmsnorm_lora_u_kernel<NB, 4>), grid, block, 0, s, h, w, eps, xn, rinv, At, u, T, D, n); break; \
   }
   switch (n / 16) {
     case 1: SMHIP_RLU(1) break;
