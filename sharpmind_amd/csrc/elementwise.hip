@@ -1007,17 +1007,34 @@ __device__ inline void adam_one(float& d, float g, float& m, float& v, float b1,
   d = d - lr * (mhat / (sqrtf(vhat) + eps) + decay * d);
 }
 
+// clip factor of Gradients.ClipGlobalNorm (Gradients.cs:92-116): 1 when no clip applies
+__device__ __forceinline__ bool adam_clip(const float* nsq, float max_norm, float& sc) {
+  if (!nsq) return false;
+  const float nrm = sqrtf(*nsq);
+  if (!(nrm > max_norm)) return false;
+  sc = max_norm / nrm;
+  return true;
+}
+
 // One float4 of each stream per thread and no grid-stride loop (one pass over the grid), with
 // non-temporal loads and stores: measured on MI355X at about 5.9 TB/s for this 4-in / 3-out
-// pattern against 5.2-5.6 TB/s for grid-stride forms.
-__global__ __launch_bounds__(kBlock) void adamw_vec_kernel(float* __restrict__ data, const float* __restrict__ grad,
+// pattern against 5.2-5.6 TB/s for grid-stride forms.  Optionally writes the bf16 shadow of the
+// new parameters and applies the global-norm clip to the gradient on the way in.
+__global__ __launch_bounds__(kBlock) void adamw_vec_kernel(float* __restrict__ data, float* __restrict__ grad,
                                                            float* __restrict__ m, float* __restrict__ v,
                                                            int64_t n4, float b1, float b2, float bc1,
-                                                           float bc2, float lr, float eps, float decay) {
+                                                           float bc2, float lr, float eps, float decay,
+                                                           uint16_t* __restrict__ shadow, const float* nsq,
+                                                           float max_norm) {
   const float omb1 = 1.f - b1, omb2 = 1.f - b2;
   const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (i >= n4) return;
   float4 d = ldnt4(data + 4 * i), g = ldnt4(grad + 4 * i), mm = ldnt4(m + 4 * i), vv = ldnt4(v + 4 * i);
+  float sc;
+  if (adam_clip(nsq, max_norm, sc)) {
+    g.x *= sc; g.y *= sc; g.z *= sc; g.w *= sc;
+    stnt4(grad + 4 * i, g);
+  }
   adam_one(d.x, g.x, mm.x, vv.x, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
   adam_one(d.y, g.y, mm.y, vv.y, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
   adam_one(d.z, g.z, mm.z, vv.z, b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
@@ -1025,29 +1042,46 @@ __global__ __launch_bounds__(kBlock) void adamw_vec_kernel(float* __restrict__ d
   stnt4(m + 4 * i, mm);
   stnt4(v + 4 * i, vv);
   stnt4(data + 4 * i, d);
+  if (shadow) {
+    const uint2 o = make_uint2((uint32_t)f2bf(d.x) | ((uint32_t)f2bf(d.y) << 16),
+                               (uint32_t)f2bf(d.z) | ((uint32_t)f2bf(d.w) << 16));
+    __builtin_nontemporal_store(o.x, reinterpret_cast<uint32_t*>(shadow + 4 * i));
+    __builtin_nontemporal_store(o.y, reinterpret_cast<uint32_t*>(shadow + 4 * i) + 1);
+  }
 }
-__global__ __launch_bounds__(kBlock) void adamw_kernel(float* __restrict__ data, const float* __restrict__ grad,
+__global__ __launch_bounds__(kBlock) void adamw_kernel(float* __restrict__ data, float* __restrict__ grad,
                                                        float* __restrict__ m, float* __restrict__ v,
                                                        int64_t i0, int64_t n, float b1, float b2, float bc1,
-                                                       float bc2, float lr, float eps, float decay) {
+                                                       float bc2, float lr, float eps, float decay,
+                                                       uint16_t* __restrict__ shadow, const float* nsq, float max_norm) {
   const float omb1 = 1.f - b1, omb2 = 1.f - b2;
-  for (int64_t i = i0 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
-    adam_one(data[i], grad[i], m[i], v[i], b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
+  float sc;
+  const bool clip = adam_clip(nsq, max_norm, sc);
+  for (int64_t i = i0 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock) {
+    float g = grad[i];
+    if (clip) grad[i] = g = g * sc;
+    adam_one(data[i], g, m[i], v[i], b1, b2, omb1, omb2, bc1, bc2, lr, eps, decay);
+    if (shadow) shadow[i] = f2bf(data[i]);
+  }
 }
 
-int adamw_update(float* data, const float* grad, float* m, float* v, int64_t n, float b1, float b2,
-                 float bc1, float bc2, float lr, float eps, float decay, hipStream_t s) {
+int adamw_update(float* data, const float* grad_, float* m, float* v, int64_t n, float b1, float b2,
+                 float bc1, float bc2, float lr, float eps, float decay, hipStream_t s, uint16_t* shadow,
+                 const float* clip_nsq, float clip_max) {
   if (n <= 0) return SMHIP_OK;
-  const bool vec = ((uintptr_t)data | (uintptr_t)grad | (uintptr_t)m | (uintptr_t)v) % 16 == 0;
+  // the gradient is written only when a clip applies
+  float* grad = const_cast<float*>(grad_);
+  const bool vec = ((uintptr_t)data | (uintptr_t)grad | (uintptr_t)m | (uintptr_t)v) % 16 == 0 &&
+                   (uintptr_t)shadow % 8 == 0;
   const int64_t n4 = vec ? n / 4 : 0;
   if (n4 > 0) {
     hipLaunchKernelGGL(adamw_vec_kernel, dim3((unsigned)((n4 + kBlock - 1) / kBlock)), dim3(kBlock), 0, s, data, grad,
-                       m, v, n4, b1, b2, bc1, bc2, lr, eps, decay);
+                       m, v, n4, b1, b2, bc1, bc2, lr, eps, decay, shadow, clip_nsq, clip_max);
     SMHIP_CHECK_LAUNCH();
   }
   if (4 * n4 < n) {  // tail (or unaligned arrays): element-wise
     hipLaunchKernelGGL(adamw_kernel, dim3(grid_for(n - 4 * n4, kBlock, 4)), dim3(kBlock), 0, s, data, grad, m, v,
-                       4 * n4, n, b1, b2, bc1, bc2, lr, eps, decay);
+                       4 * n4, n, b1, b2, bc1, bc2, lr, eps, decay, shadow, clip_nsq, clip_max);
     SMHIP_CHECK_LAUNCH();
   }
   return SMHIP_OK;
@@ -1056,15 +1090,25 @@ int adamw_update(float* data, const float* grad, float* m, float* v, int64_t n, 
 // ============================================================================
 // L2 norm squared (TrainingKernels.cs:94-135): double partials per block, fixed-order final sum
 // ============================================================================
-__global__ __launch_bounds__(kBlock) void l2_partial_kernel(const float* __restrict__ x, int64_t n,
+// float4 loads when x is 16-byte aligned (elements [0, 4 n4) by vectors, the rest one by one);
+// each element contributes (double)(v * v) as in the reference
+__global__ __launch_bounds__(kBlock) void l2_partial_kernel(const float* __restrict__ x, int64_t n, int64_t n4,
                                                             double* __restrict__ part) {
   __shared__ double sh[kBlock / 64];
-  double a = 0.0;
-  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock) {
-    float v = x[i];
+  double a = 0.0, b = 0.0;
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
+    const float4 v = ldnt4(x + 4 * i);
+    a += (double)(v.x * v.x);
+    b += (double)(v.y * v.y);
+    a += (double)(v.z * v.z);
+    b += (double)(v.w * v.w);
+  }
+  for (int64_t i = 4 * n4 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+    const float v = x[i];
     a += (double)(v * v);
   }
-  a = wave_sum_d(a);
+  a = wave_sum_d(a + b);
   if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = a;
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -1073,21 +1117,28 @@ __global__ __launch_bounds__(kBlock) void l2_partial_kernel(const float* __restr
     part[blockIdx.x] = r;
   }
 }
-__global__ void l2_final_kernel(const double* __restrict__ part, int G, float* __restrict__ out,
-                                int accumulate) {
-  if (threadIdx.x == 0 && blockIdx.x == 0) {
-    double r = 0.0;
-    for (int g = 0; g < G; g++) r += part[g];
-    *out = accumulate ? (float)((double)*out + r) : (float)r;
+// 256 threads sum strided shares of the partials, then a fixed-order tree (deterministic)
+__global__ __launch_bounds__(256) void l2_final_kernel(const double* __restrict__ part, int G, float* __restrict__ out,
+                                                       int accumulate) {
+  __shared__ double sh[256];
+  double r = 0.0;
+  for (int g = threadIdx.x; g < G; g += 256) r += part[g];
+  sh[threadIdx.x] = r;
+  __syncthreads();
+  for (int h = 128; h > 0; h >>= 1) {
+    if ((int)threadIdx.x < h) sh[threadIdx.x] += sh[threadIdx.x + h];
+    __syncthreads();
   }
+  if (threadIdx.x == 0) *out = accumulate ? (float)((double)*out + sh[0]) : (float)sh[0];
 }
 
 int l2normsq(const float* x, int64_t n, float* out, int accumulate, hipStream_t s) {
-  int G = grid_for(n > 0 ? n : 1, kBlock, 4);
+  const int64_t n4 = (uintptr_t)x % 16 == 0 ? n / 4 : 0;
+  int G = grid_for(std::max<int64_t>(n4, n - 4 * n4) > 0 ? std::max<int64_t>(n4, n - 4 * n4) : 1, kBlock, 8);
   double* part = (double*)workspace(s, sizeof(double) * G, 2);
   if (!part) return fail(SMHIP_ENOMEM, "l2normsq: workspace");
-  hipLaunchKernelGGL(l2_partial_kernel, dim3(G), dim3(kBlock), 0, s, x, n, part);
-  hipLaunchKernelGGL(l2_final_kernel, dim3(1), dim3(64), 0, s, part, G, out, accumulate);
+  hipLaunchKernelGGL(l2_partial_kernel, dim3(G), dim3(kBlock), 0, s, x, n, n4, part);
+  hipLaunchKernelGGL(l2_final_kernel, dim3(1), dim3(256), 0, s, part, G, out, accumulate);
   SMHIP_CHECK_LAUNCH();
   return SMHIP_OK;
 }
@@ -1105,28 +1156,61 @@ int scale_inplace(float* x, int64_t n, float sc, hipStream_t s) {
 
 // ============================================================================
 // Embedding backward (GradientKernels.Embedding_Scalar, GradientKernels.cs:490-506)
-// Deterministic and bit-identical to the reference: the block owning the first
-// occurrence of an id adds every occurrence's row into dE[id] in token order.
+// Deterministic and bit-identical to the reference: dE[id] receives every occurrence's row in
+// token order, starting from its current value.  Pass 1 links each token to the next token with
+// the same id (nxt) and marks the first occurrence (ids compared through LDS tiles, one thread
+// per token); pass 2 walks each first occurrence's chain, D columns spread over the block.
 // ============================================================================
+// 64 tokens per workgroup (one per lane); the four waves scan quarters of each 1024-id LDS tile
+// (four ids per LDS read) and combine through LDS
+__global__ __launch_bounds__(kBlock) void embedding_links_kernel(const int32_t* __restrict__ ids, int T,
+                                                                 int2* __restrict__ link) {
+  __shared__ __attribute__((aligned(16))) int32_t tile[1024];
+  __shared__ int sfirst[4][64], snxt[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int t = blockIdx.x * 64 + lane;
+  const int id = t < T ? ids[t] : INT_MIN;
+  int nxt = INT_MAX;
+  bool first = true;
+  for (int base = 0; base < T; base += 1024) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < 1024; i += kBlock) tile[i] = base + i < T ? ids[base + i] : INT_MIN;
+    __syncthreads();
+    const int lo = 256 * w, hi = min(lo + 256, T - base);
+    for (int i = lo; i < hi; i += 4) {
+      const int4 q = *reinterpret_cast<const int4*>(tile + i);
+      const int qq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int u = base + i + k;
+        if (qq[k] == id && u < T) {
+          if (u < t) first = false;
+          else if (u > t) nxt = min(nxt, u);
+        }
+      }
+    }
+  }
+  sfirst[w][lane] = first;
+  snxt[w][lane] = nxt;
+  __syncthreads();
+  if (w == 0 && t < T) {
+    const bool f = sfirst[0][lane] && sfirst[1][lane] && sfirst[2][lane] && sfirst[3][lane];
+    const int n = min(min(snxt[0][lane], snxt[1][lane]), min(snxt[2][lane], snxt[3][lane]));
+    link[t] = make_int2(f ? 1 : 0, n == INT_MAX ? -1 : n);
+  }
+}
+
 __global__ __launch_bounds__(kBlock) void embedding_bwd_kernel(const float* __restrict__ dY,
                                                                const int32_t* __restrict__ ids,
+                                                               const int2* __restrict__ link,
                                                                float* __restrict__ dE, int T,
                                                                int D, int V) {
-  __shared__ int dup;
   for (int t = blockIdx.x; t < T; t += gridDim.x) {
     const int id = ids[t];
-    if (threadIdx.x == 0) dup = 0;
-    __syncthreads();
-    for (int u = threadIdx.x; u < t; u += kBlock)
-      if (ids[u] == id) dup = 1;
-    __syncthreads();
-    const int is_dup = dup;
-    __syncthreads();
-    if (is_dup || id < 0 || id >= V) continue;
+    if (!link[t].x || id < 0 || id >= V) continue;
     for (int d = threadIdx.x; d < D; d += kBlock) {
       float acc = dE[(int64_t)id * D + d];
-      for (int u = t; u < T; u++)
-        if (ids[u] == id) acc = acc + dY[(int64_t)u * D + d];
+      for (int u = t; u >= 0; u = link[u].y) acc = acc + dY[(int64_t)u * D + d];
       dE[(int64_t)id * D + d] = acc;
     }
   }
@@ -1135,7 +1219,10 @@ __global__ __launch_bounds__(kBlock) void embedding_bwd_kernel(const float* __re
 int embedding_backward(const float* dY, const int32_t* ids, float* dE, int T, int D, int V,
                        hipStream_t s) {
   if (T <= 0) return SMHIP_OK;
-  hipLaunchKernelGGL(embedding_bwd_kernel, dim3(grid_for(T, 1, 8)), dim3(kBlock), 0, s, dY, ids,
+  int2* link = (int2*)workspace(s, sizeof(int2) * (size_t)T, 10);
+  if (!link) return fail(SMHIP_ENOMEM, "embedding backward: workspace");
+  hipLaunchKernelGGL(embedding_links_kernel, dim3(ceil_div(T, 64)), dim3(kBlock), 0, s, ids, T, link);
+  hipLaunchKernelGGL(embedding_bwd_kernel, dim3(grid_for(T, 1, 8)), dim3(kBlock), 0, s, dY, ids, link,
                      dE, T, D, V);
   SMHIP_CHECK_LAUNCH();
   return SMHIP_OK;

@@ -753,20 +753,21 @@ static int optimizer_step(Engine* e, hipStream_t s) {
   const smhip_model_config& c = e->c;
   int rc;
   e->step++;
-  if (c.max_grad_norm > 0.f) {  // TrainLoop.cs:125-127 -> Gradients.ClipGlobalNorm
-    if ((rc = l2normsq(e->grad, e->n_train, e->gnorm, 0, s))) return rc;
-    if ((rc = clip_grads(e->grad, e->n_train, e->gnorm, c.max_grad_norm, s))) return rc;
-  }
+  // TrainLoop.cs:125-127 -> Gradients.ClipGlobalNorm: the norm here, the scaling inside the AdamW
+  // pass (which also refreshes the bf16 shadows of bf16 engines)
+  const bool clip = c.max_grad_norm > 0.f;
+  if (clip && (rc = l2normsq(e->grad, e->n_train, e->gnorm, 0, s))) return rc;
+  const float* nsq = clip ? e->gnorm : nullptr;
   // AdamW.Update (AdamW.cs:52-89): bc_i = 1 - beta_i^t ; decayed tensors first, then no-decay
   const float bc1 = 1.f - powf(c.beta1, (float)e->step), bc2 = 1.f - powf(c.beta2, (float)e->step);
   if ((rc = adamw_update(e->train, e->grad, e->m, e->v, e->n_decay, c.beta1, c.beta2, bc1, bc2, c.lr, c.adam_eps,
-                         c.weight_decay, s)))
+                         c.weight_decay, s, e->train_bf, nsq, c.max_grad_norm)))
     return rc;
   if (e->n_train > e->n_decay)
     if ((rc = adamw_update(e->train + e->n_decay, e->grad + e->n_decay, e->m + e->n_decay, e->v + e->n_decay,
-                           e->n_train - e->n_decay, c.beta1, c.beta2, bc1, bc2, c.lr, c.adam_eps, 0.f, s)))
+                           e->n_train - e->n_decay, c.beta1, c.beta2, bc1, bc2, c.lr, c.adam_eps, 0.f, s,
+                           e->train_bf ? e->train_bf + e->n_decay : nullptr, nsq, c.max_grad_norm)))
       return rc;
-  if (e->train_bf) return cast_bf16(e->train, e->train_bf, e->n_train, s);
   return SMHIP_OK;
 }
 

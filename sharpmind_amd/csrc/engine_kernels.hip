@@ -153,14 +153,32 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_kernel(
   }
 }
 
-__global__ void colsum_add2_kernel(const float* __restrict__ part, float* __restrict__ dq,
-                                   float* __restrict__ dk, int G, int D) {
-  int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= 2 * D) return;
-  float s = 0.f;
-  for (int g = 0; g < G; g++) s += part[(int64_t)g * 2 * D + c];
-  float* dst = c < D ? dq + c : dk + (c - D);
-  *dst += s;
+// dq[c] += sum_g part[g][c] (c < D), dk[c - D] += ... (c >= D): 64 columns per workgroup,
+// 16 row groups of 64 lanes each sum a strided share of the G partial rows (coalesced 256-byte
+// rows), then the 16 group sums combine in a fixed order (deterministic)
+__global__ __launch_bounds__(1024) void colsum_add2_kernel(const float* __restrict__ part, float* __restrict__ dq,
+                                                           float* __restrict__ dk, int G, int D) {
+  __shared__ float sh[16][64];
+  const int l = threadIdx.x & 63, rg = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + l;
+  float s0 = 0.f, s1 = 0.f;
+  if (c < 2 * D) {
+    int g = rg;
+    for (; g + 16 < G; g += 32) {
+      s0 += part[(int64_t)g * 2 * D + c];
+      s1 += part[(int64_t)(g + 16) * 2 * D + c];
+    }
+    if (g < G) s0 += part[(int64_t)g * 2 * D + c];
+  }
+  sh[rg][l] = s0 + s1;
+  __syncthreads();
+  if (rg == 0 && c < 2 * D) {
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < 16; q++) s += sh[q][l];
+    float* dst = c < D ? dq + c : dk + (c - D);
+    *dst += s;
+  }
 }
 
 // ---------------------------------------------------------------- vectorised form, D = 64 / 128
@@ -503,7 +521,7 @@ int qkv_prep_backward(const void* dq_, const void* dk_, const void* dv_, int gra
     hipLaunchKernelGGL(qkv_prep_bwd_kernel<float>, dim3(g), dim3(256), 0, s, dq, dk, dv, (const float*)qkv, rinv, wq, wk, cosT, sinT, (float*)dqkv, part, T, S, Hq, Hkv, D, qk_norm, neox);
   SMHIP_CHECK_LAUNCH();
   if (part) {
-    hipLaunchKernelGGL(colsum_add2_kernel, dim3(ceil_div(2 * D, 256)), dim3(256), 0, s, part, dwq, dwk, g, D);
+    hipLaunchKernelGGL(colsum_add2_kernel, dim3(ceil_div(2 * D, 64)), dim3(1024), 0, s, part, dwq, dwk, g, D);
     SMHIP_CHECK_LAUNCH();
   }
   return SMHIP_OK;
@@ -636,22 +654,6 @@ __global__ void lora_mask_kernel(float* __restrict__ dB, int nr, int r, int Out,
 }
 int lora_mask(float* dB, int nr, int r, int Out, const int* col_starts_dev, int nblocks, hipStream_t s) {
   hipLaunchKernelGGL(lora_mask_kernel, dim3(gridn((int64_t)nr * Out)), dim3(256), 0, s, dB, nr, r, Out, col_starts_dev, nblocks);
-  SMHIP_CHECK_LAUNCH();
-  return SMHIP_OK;
-}
-
-// ============================================================================
-// clipping (Gradients.ClipGlobalNorm, Gradients.cs:92-116): if ||g|| > max, g *= max/||g||
-// norm_sq is a device float holding sum g^2 (smhip l2normsq), also exported for logging.
-// ============================================================================
-__global__ void clip_kernel(float* __restrict__ g, int64_t n, const float* __restrict__ norm_sq, float max_norm) {
-  const float nrm = sqrtf(*norm_sq);
-  if (!(nrm > max_norm)) return;
-  const float sc = max_norm / nrm;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) g[i] *= sc;
-}
-int clip_grads(float* g, int64_t n, const float* norm_sq, float max_norm, hipStream_t s) {
-  hipLaunchKernelGGL(clip_kernel, dim3(gridn(n)), dim3(256), 0, s, g, n, norm_sq, max_norm);
   SMHIP_CHECK_LAUNCH();
   return SMHIP_OK;
 }

@@ -30,8 +30,12 @@ int ce_softmax_grad_bf16(const float* logits, const int32_t* labels, uint16_t* d
 // pairs over consecutive column blocks): the logits are read once; no label smoothing
 int ce_softmax_grad_bf16_stats(const float* logits, const float* stats, int nst, const int32_t* labels, uint16_t* dL,
                                float* loss, int T, int V, int ignoreId, hipStream_t s);
+// shadow: optional bf16 copy of the updated parameters; clip_nsq: optional device sum of squares
+// of the whole gradient -- when sqrt(*clip_nsq) > clip_max the gradient is first scaled by
+// clip_max / sqrt(*clip_nsq) (and stored back scaled), as a separate clip pass would
 int adamw_update(float* data, const float* grad, float* m, float* v, int64_t n, float b1, float b2,
-                 float bc1, float bc2, float lr, float eps, float decay, hipStream_t s);
+                 float bc1, float bc2, float lr, float eps, float decay, hipStream_t s, uint16_t* shadow = nullptr,
+                 const float* clip_nsq = nullptr, float clip_max = 0.f);
 int l2normsq(const float* x, int64_t n, float* out, int accumulate, hipStream_t s);
 int scale_inplace(float* x, int64_t n, float sc, hipStream_t s);
 int embedding_backward(const float* dY, const int32_t* ids, float* dE, int T, int D, int V,
@@ -156,7 +160,6 @@ int qkv_prep_backward(const void* dq, const void* dk, const void* dv, int grads_
 int swiglu_fused_forward(const void* gu, void* act, int T, int F, int bf16, hipStream_t s);
 int swiglu_fused_backward(const void* dA, const void* gu, void* dgu, int T, int F, int bf16, hipStream_t s);
 int lora_mask(float* dB, int nr, int r, int Out, const int* col_starts_dev, int nblocks, hipStream_t s);
-int clip_grads(float* g, int64_t n, const float* norm_sq, float max_norm, hipStream_t s);
 int cast_bf16(const float* x, uint16_t* y, int64_t n, hipStream_t s);
 int fill_normal(float* x, int64_t n, uint64_t seed, float mean, float std, hipStream_t s);
 int fill_uniform(float* x, int64_t n, uint64_t seed, float lo, float hi, hipStream_t s);
