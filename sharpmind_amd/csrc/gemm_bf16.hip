@@ -235,6 +235,7 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
     const bool sk = skinny(g.M, g.N);
     // at most one 128x128 tile per CU and a moderate K: the 8-wave tile (two waves per SIMD
     // hide LDS and barrier latency) with a ring, whole K per workgroup, beats split-K
+    // (k-contiguous operands only: with a row-contiguous operand split-K measured faster)
     const bool w8 = tile == T128x128 && am == SRC_BF16_K && bm == SRC_BF16_K && !sk &&
                     (int64_t)ceil_div(g.M, 128) * ceil_div(g.N, 128) <= num_cus() && nk < 96;
     if (w8) tile = T128x128W8;

@@ -11,8 +11,9 @@
 // is bank-conflict free.  Operand staging by mode (template parameters):
 //   BF16_K   k-contiguous bf16: buffer_load ... lds (direct global -> LDS, no registers);
 //            each lane fetches the global chunk that belongs at its swizzled LDS slot;
-//   BF16_R   row-contiguous bf16: 4 k-rows x 8 columns per thread, transposed in
-//            registers, written as 8-byte LDS quads;
+//   BF16_R   row-contiguous bf16: buffer_load ... lds of the tile as it lies in memory
+//            (64 k-rows, chunks swizzled by k-row), MFMA fragments read with
+//            ds_read_b64_tr_b16 (two per fragment);
 //   Q8_K / Q4K_K   frozen base rows, Q8T / Q4KT   the same values as column planes
 //            (transposed copy for dX = dY W): int8 / 4-bit codes and their fp32 scales are
 //            loaded into registers and decoded (q*d, or (sc*d)*v - mn*dmin: the exact fp32
@@ -85,6 +86,11 @@ __device__ __forceinline__ float as_f(uint32_t w) { return __builtin_bit_cast(fl
 // swizzled position is that slot.
 template <int ROWS, int NT>
 struct DmaLoad {
+  static constexpr bool TR = false;
+  // fragment of rows rb .. rb+31, k-slice kk, from the [row][64] layout
+  static __device__ __forceinline__ bf16x8 frag(const uint8_t* tile, int rb, int kk, int lane) {
+    return *reinterpret_cast<const bf16x8*>(tile + sw(rb + (lane & 31), 2 * kk + (lane >> 5)));
+  }
   static constexpr int NW = NT / 64;
   static_assert((ROWS / 8) % NW == 0, "tile rows must split evenly over the waves");
   static constexpr int NI = ROWS / 8 / NW;  // instructions per wave per tile
@@ -111,53 +117,70 @@ struct DmaLoad {
   __device__ __forceinline__ void commit(uint8_t*) {}
 };
 
-// ---------------------------------------------------------------- BF16_R: k-strided, transposed in registers
-// quad = 4 consecutive k x 8 consecutive rows; (ROWS/8)*16 quads per tile.
+// ---------------------------------------------------------------- BF16_R: direct to LDS, read transposed
+// The tile is kept as it lies in memory: 64 k-rows of ROWS bf16 (2 ROWS bytes each), 16-byte
+// chunk c of k-row k at slot c ^ tsw(k).  One wave instruction moves 1 KiB; lane l lands at byte
+// 16 l of the instruction's block and loads the global chunk that belongs there.  The MFMA
+// fragment (8 consecutive k of one row) is two ds_read_b64_tr_b16: over the 16 lanes of a
+// group, source lane s names 4 rows (m) of k-row kb + s/4 and destination lane s receives row
+// mb + s of those 4 k-rows.  A 32-lane half reads 4 k-rows x 64 bytes; the swizzle puts them on
+// 16 distinct 16-byte bank groups (a k-row is 0 or 8 bank groups mod 16, by ROWS).
+template <int ROWS>
+__device__ __forceinline__ int tsw(int k) {
+  if constexpr ((ROWS / 8) % 16 == 0) return (k & 3) << 2;
+  else return ((k >> 1) & 1) << 2;
+}
+typedef short gshort4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) gshort4 lds_gs4;
+
 template <int ROWS, int NT>
-struct RLoad {
-  static constexpr int RG = ROWS / 8;
-  static constexpr int NQ_ALL = RG * (BK / 4);
-  static constexpr int NQ = NQ_ALL >= NT ? NQ_ALL / NT : 1;
-  u32x4 v[NQ][4];
-  uint32_t off[NQ];
-  uint32_t ldb;  // bytes per k row
+struct DmaTLoad {
+  static_assert((ROWS / 8) % 16 == 0 || (ROWS / 8) % 16 == 8, "k-row must be a multiple of 128 bytes");
+  static constexpr bool TR = true;
+  static constexpr int NW = NT / 64;
+  static_assert((ROWS / 8) % NW == 0, "tile blocks must split evenly over the waves");
+  static constexpr int NI = ROWS / 8 / NW;  // instructions per wave per tile
+  uint32_t off[NI];
+  uint32_t ldb;  // bytes per k-row of the operand
   __amdgpu_buffer_rsrc_t rs;
-  __device__ __forceinline__ bool active(int q) const { return NQ_ALL >= NT || (int)threadIdx.x < NQ_ALL; }
-  __device__ __forceinline__ void init(const Op& o, int r0, int R) {
+  __device__ __forceinline__ void init(const Op& o, int r0, int) {
     rs = rsrc(o.p, o.bytes);
     ldb = (uint32_t)(o.ld * 2);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
 #pragma unroll
-    for (int q = 0; q < NQ; q++) {
-      const int id = q * NT + threadIdx.x;
-      const int rg = id % RG, kq = id / RG;
-      off[q] = (uint32_t)(((int64_t)(kq * 4) * o.ld + r0 + rg * 8) * 2);
+    for (int j = 0; j < NI; j++) {
+      const int b = (j * NW + w) * 1024 + 16 * l;
+      const int k = b / (ROWS * 2), slot = (b % (ROWS * 2)) >> 4;
+      const int c = slot ^ tsw<ROWS>(k);
+      off[j] = (uint32_t)(((int64_t)k * o.ld + r0 + 8 * c) * 2);
     }
   }
-  __device__ __forceinline__ void fetch(uint8_t*, int k0) {
+  __device__ __forceinline__ void fetch(uint8_t* tile, int k0) {
+    const int w = threadIdx.x >> 6;
     const uint32_t kb = (uint32_t)k0 * ldb;
+#if defined(__HIP_DEVICE_COMPILE__)
 #pragma unroll
-    for (int q = 0; q < NQ; q++) {
-      if (!active(q)) continue;
-#pragma unroll
-      for (int j = 0; j < 4; j++) v[q][j] = __builtin_amdgcn_raw_buffer_load_b128(rs, off[q] + kb + j * ldb, 0, 0);
-    }
+    for (int j = 0; j < NI; j++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(tile + (j * NW + w) * 1024), 16, off[j] + kb, 0, 0, 0);
+#endif
   }
-  __device__ __forceinline__ void commit(uint8_t* tile) {
-#pragma unroll
-    for (int q = 0; q < NQ; q++) {
-      if (!active(q)) continue;
-      const int id = q * NT + threadIdx.x;
-      const int rg = id % RG, kq = id / RG;
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const int w = i >> 1, hi = i & 1;
-        auto el = [&](int j) -> uint32_t { return hi ? (v[q][j][w] >> 16) : (v[q][j][w] & 0xFFFFu); };
-        u32x2 d;
-        d[0] = el(0) | (el(1) << 16);
-        d[1] = el(2) | (el(3) << 16);
-        *reinterpret_cast<u32x2*>(tile + sw(rg * 8 + i, kq >> 1) + (kq & 1) * 8) = d;
-      }
-    }
+  __device__ __forceinline__ void commit(uint8_t*) {}
+  // fragment of rows rb .. rb+31 (rb a multiple of 32), k-slice kk (16 k): lane l holds row
+  // rb + l%32, k 16 kk + 8 (l/32) .. +7
+  static __device__ __forceinline__ bf16x8 frag(const uint8_t* tile, int rb, int kk, int lane) {
+    const int g = lane >> 4, s = lane & 15;
+    const int k = kk * 16 + 8 * (g >> 1) + (s >> 2);
+    const int c = ((rb + 16 * (g & 1)) >> 3) + ((s & 3) >> 1);
+    const uint8_t* p = tile + k * (ROWS * 2) + ((c ^ tsw<ROWS>(k)) << 4) + (s & 1) * 8;
+    gshort4 lo, hi;
+#if defined(__HIP_DEVICE_COMPILE__)
+    lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_gs4*)p);
+    hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_gs4*)(p + 4 * ROWS * 2));
+#else
+    lo = hi = gshort4{};
+#endif
+    const uint2 x = __builtin_bit_cast(uint2, lo), y = __builtin_bit_cast(uint2, hi);
+    return __builtin_bit_cast(bf16x8, make_uint4(x.x, x.y, y.x, y.y));
   }
 };
 
@@ -165,6 +188,11 @@ struct RLoad {
 // unit = 16 consecutive k of one row (one 16-byte int8 load, or 8 bytes of 4-bit codes)
 template <int MODE, int ROWS, int NT>
 struct QLoad {
+  static constexpr bool TR = false;
+  // fragment of rows rb .. rb+31, k-slice kk, from the [row][64] layout
+  static __device__ __forceinline__ bf16x8 frag(const uint8_t* tile, int rb, int kk, int lane) {
+    return *reinterpret_cast<const bf16x8*>(tile + sw(rb + (lane & 31), 2 * kk + (lane >> 5)));
+  }
   static constexpr int NU = ROWS * 4 / NT;
   static_assert(NU >= 1, "quantised operand tile needs >= 64 rows");
   static constexpr bool Q8 = MODE == SRC_Q8_K || MODE == SRC_Q8T;
@@ -273,7 +301,7 @@ template <int MODE, int ROWS, int NT>
 struct LoaderFor {
   using T = typename std::conditional<
       MODE == SRC_BF16_K, DmaLoad<ROWS, NT>,
-      typename std::conditional<MODE == SRC_BF16_R, RLoad<ROWS, NT>, QLoad<MODE, ROWS, NT>>::type>::type;
+      typename std::conditional<MODE == SRC_BF16_R, DmaTLoad<ROWS, NT>, QLoad<MODE, ROWS, NT>>::type>::type;
 };
 
 // ---------------------------------------------------------------- rank-extension tile (LoRA)
@@ -510,8 +538,10 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW, ST>::OCC)) void ge
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
-  typename LoaderFor<AMODE, BM, NT>::T la;
-  typename LoaderFor<BMODE, BN, NT>::T lb;
+  using LA = typename LoaderFor<AMODE, BM, NT>::T;
+  using LB = typename LoaderFor<BMODE, BN, NT>::T;
+  LA la;
+  LB lb;
   la.init(g.A, m0, g.M);
   lb.init(g.B, n0, g.N);
 
@@ -524,16 +554,25 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW, ST>::OCC)) void ge
   // fragments of k-slice kk+1 are read from LDS while the MFMAs of slice kk run
   // mid() runs once the first fragments of the tile are requested (it issues the next
   // tile's global loads, overlapping their issue with the LDS round trip)
-  auto compute = [&](int buf, auto&& mid) {
+  // tr: the stage holds the main loaders' tiles (a transposed-read layout for row-contiguous
+  // operands); false for the rank-extension tiles, which are always [row][64]
+  auto compute = [&](int buf, auto&& mid, auto tr) {
+    constexpr bool TA = decltype(tr)::value && LA::TR, TB = decltype(tr)::value && LB::TR;
     const uint8_t* a = sA(buf);
     const uint8_t* b = sB(buf);
     bf16x8 fa[2][MB], fb[2][NB];
     auto rd = [&](int kk, int p) {
       const int ch = 2 * kk + (lane >> 5);
 #pragma unroll
-      for (int i = 0; i < MB; i++) fa[p][i] = *reinterpret_cast<const bf16x8*>(a + sw(wm * S::WM + i * 32 + (lane & 31), ch));
+      for (int i = 0; i < MB; i++) {
+        if constexpr (TA) fa[p][i] = LA::frag(a, wm * S::WM + i * 32, kk, lane);
+        else fa[p][i] = *reinterpret_cast<const bf16x8*>(a + sw(wm * S::WM + i * 32 + (lane & 31), ch));
+      }
 #pragma unroll
-      for (int j = 0; j < NB; j++) fb[p][j] = *reinterpret_cast<const bf16x8*>(b + sw(wn * S::WN + j * 32 + (lane & 31), ch));
+      for (int j = 0; j < NB; j++) {
+        if constexpr (TB) fb[p][j] = LB::frag(b, wn * S::WN + j * 32, kk, lane);
+        else fb[p][j] = *reinterpret_cast<const bf16x8*>(b + sw(wn * S::WN + j * 32 + (lane & 31), ch));
+      }
     };
     rd(0, 0);
     mid();
@@ -559,7 +598,7 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW, ST>::OCC)) void ge
     ext_tile<BM, NT>(g.amode2, g.ext_vec != 0, g.A2, m0, t * BK, g.M, g.K2, g.alpha2, sA(buf));
     ext_tile<BN, NT>(g.bmode2, g.ext_vec != 0, g.B2, n0, t * BK, g.N, g.K2, 1.f, sB(buf));
     __syncthreads();
-    compute(buf, [] {});
+    compute(buf, [] {}, std::false_type{});
     __syncthreads();
   };
 
@@ -567,7 +606,8 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW, ST>::OCC)) void ge
     // ST-stage ring (direct-to-LDS operands only): tiles t+1 .. t+ST-2 are in flight while
     // tile t is multiplied; the barrier at the top of iteration t also frees the stage of
     // tile t-1, which is refilled with tile t+ST-1
-    static_assert(AMODE == SRC_BF16_K && BMODE == SRC_BF16_K, "the ring stages direct-to-LDS operands only");
+    static_assert((AMODE == SRC_BF16_K || AMODE == SRC_BF16_R) && (BMODE == SRC_BF16_K || BMODE == SRC_BF16_R),
+                  "the ring stages direct-to-LDS operands only");
     constexpr int PER = decltype(la)::NI + decltype(lb)::NI;  // DMA instructions per wave per tile
 #pragma unroll
     for (int t = 0; t < ST - 1; t++)
@@ -587,7 +627,7 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW, ST>::OCC)) void ge
           la.fetch(sA(st), (kt0 + t + ST - 1) * BK);
           lb.fetch(sB(st), (kt0 + t + ST - 1) * BK);
         }
-      });
+      }, std::true_type{});
     }
   } else if (nk1 > 0) {
     la.fetch(sA(0), kt0 * BK);
@@ -605,7 +645,7 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW, ST>::OCC)) void ge
           la.fetch(sA(buf ^ 1), (kt0 + t + 1) * BK);
           lb.fetch(sB(buf ^ 1), (kt0 + t + 1) * BK);
         }
-      });
+      }, std::true_type{});
       if (more) {
         la.commit(sA(buf ^ 1));
         lb.commit(sB(buf ^ 1));
@@ -661,7 +701,7 @@ static void launch_main(Kern k, const dim3& grid, const dim3& block, hipStream_t
 template <int BM, int BN, int WGM, int NW, int AM, int BMD, int TAG>
 static void launch_c(const Args& a, int c_bf16, int splits, hipStream_t s) {
   const dim3 grid(a.tiles_m * a.tiles_n, splits);
-  if constexpr (AM == SRC_BF16_K && BMD == SRC_BF16_K && BM + BN <= 256) {
+  if constexpr ((AM == SRC_BF16_K || AM == SRC_BF16_R) && (BMD == SRC_BF16_K || BMD == SRC_BF16_R) && BM + BN <= 256) {
     const int st = ring_stages(NW);
     if (st == 3 || st == 4) {
       if (c_bf16 && !a.partial) {
