@@ -411,8 +411,11 @@ struct Shape {
 // (e/4)*8 + (lane>>5)*4 + e%4 of each 32x32 accumulator block.
 // FULL: the caller guarantees whole tiles (M % BM == 0, N % BN == 0); the general path is not
 // compiled in (its register demand would otherwise shape the whole kernel's allocation)
+// Rl: the tile's residual rows already copied to LDS ([BM][BN] fp32; whole tiles only), read
+// there instead of from global memory
 template <class S, bool C_BF16, bool FULL = false>
-__device__ __forceinline__ void gemm_epilogue(const Args& g, floatx16 (&acc)[S::MB][S::NB], int m0, int n0, int split) {
+__device__ __forceinline__ void gemm_epilogue(const Args& g, floatx16 (&acc)[S::MB][S::NB], int m0, int n0, int split,
+                                              const float* Rl = nullptr) {
   constexpr int MB = S::MB, NB = S::NB, BM = S::WM * (S::NT / 64 / S::WGN), BN = S::WN * S::WGN;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int wm = wv / S::WGN, wn = wv % S::WGN;
@@ -440,12 +443,18 @@ __device__ __forceinline__ void gemm_epilogue(const Args& g, floatx16 (&acc)[S::
               *c = f2bf(o);
             } else {
               float* c = (float*)g.C + row * g.ldc + col;
-              if constexpr (decltype(has_r)::value) o = o + g.R[row * g.ldr + col];
+              if constexpr (decltype(has_r)::value == 2) o = o + Rl[(row - m0) * BN + (col - n0)];
+              else if constexpr (decltype(has_r)::value == 1) o = o + g.R[row * g.ldr + col];
               if constexpr (decltype(has_beta)::value) o = o + g.beta * *c;
               *c = o;
             }
             // one 32x32 block at a time: hoisting every block's R / C loads spills the accumulators
-            if ((e & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+            // (the compiler fence also keeps LDS residual reads, which cannot alias the stores,
+            // from being hoisted together)
+            if ((e & 3) == 3) {
+              asm volatile("" ::: "memory");
+              __builtin_amdgcn_sched_barrier(0);
+            }
           }
       }
     };
@@ -463,6 +472,10 @@ __device__ __forceinline__ void gemm_epilogue(const Args& g, floatx16 (&acc)[S::
       return;
     }
     const bool bias = g.bias != nullptr, r = !C_BF16 && g.R != nullptr, beta = g.beta != 0.f;
+    if (r && Rl && !bias && !beta) {
+      store(F{}, std::integral_constant<int, 2>{}, F{});
+      return;
+    }
     if (!bias && !r && !beta) store(F{}, F{}, F{});
     else if (!bias && r && !beta) store(F{}, T{}, F{});
     else if (!bias && !r && beta) store(F{}, F{}, T{});
@@ -657,7 +670,28 @@ __global__ __launch_bounds__(64 * NW, (Shape<BM, BN, WGM, NW, ST>::OCC)) void ge
   if (nk1 == 0)
     for (int t = 0; t < nk2; t++) ext_step(0, t);
 
-  gemm_epilogue<S, C_BF16>(g, acc, m0, n0, split);
+  // fp32 C with a residual: the tile's R rows are copied to the idle LDS stages first (one
+  // coalesced burst), so the epilogue does not wait on memory between its stores
+  const float* rl = nullptr;
+  if constexpr (!C_BF16 && BM * BN * 4 <= S::LDS && (BN * 4) <= 1024 && 1024 % (BN * 4) == 0) {
+    if (g.R && g.beta == 0.f && !g.partial && m0 + BM <= g.M && n0 + BN <= g.N) {
+      __syncthreads();
+#if defined(__HIP_DEVICE_COMPILE__)
+      const __amdgpu_buffer_rsrc_t rr =
+          rsrc(g.R + (int64_t)m0 * g.ldr + n0, (int)(((int64_t)(BM - 1) * g.ldr + BN) * 4));
+      constexpr int RPI = 1024 / (BN * 4);  // tile rows per 1 KiB copy
+      for (int i = wv; i < BM / RPI; i += NW) {
+        const int row = i * RPI + lane / (BN / 4), c4 = lane % (BN / 4);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void*)(smem + i * 1024), 16,
+                                                 (uint32_t)((row * g.ldr + 4 * c4) * 4), 0, 0, 0);
+      }
+#endif
+      wait_vm();
+      __syncthreads();
+      rl = reinterpret_cast<const float*>(smem);
+    }
+  }
+  gemm_epilogue<S, C_BF16>(g, acc, m0, n0, split, rl);
 }
 
 // ---------------------------------------------------------------- host dispatch

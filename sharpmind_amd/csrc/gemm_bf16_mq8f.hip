@@ -568,7 +568,32 @@ __global__ __launch_bounds__(64 * (NWM + NWD + NWL), 1) void gemm_q8f_kernel(Arg
       ring_barrier();
     }
   }
-  if (role == 0) gemm_epilogue<S, C_BF16, FULL>(g, acc, m0, n0, split);
+  // fp32 C with a residual (y = x W^T + R): every wave copies a share of the tile's R rows to
+  // the now idle LDS ring with buffer_load ... lds before the epilogue, so the MFMA waves add R
+  // from LDS (one coalesced burst per workgroup instead of a memory round trip per few
+  // elements between the C stores)
+  const float* rl = nullptr;
+  if constexpr (!C_BF16) {
+    if (g.R && g.beta == 0.f && !g.partial && m0 + BM <= g.M && n0 + BN <= g.N) {
+      static_assert(BM * BN * 4 <= LDS, "residual tile fits the LDS ring");
+      ring_barrier();  // every role is done with the ring
+#if defined(__HIP_DEVICE_COMPILE__)
+      const __amdgpu_buffer_rsrc_t rr =
+          rsrc(g.R + (int64_t)m0 * g.ldr + n0, (int)(((int64_t)(BM - 1) * g.ldr + BN) * 4));
+      constexpr int RPI = 1024 / (BN * 4);  // tile rows per 1 KiB copy
+      constexpr int NI = BM / RPI;
+      for (int i = wv; i < NI; i += NT / 64) {
+        const int row = i * RPI + lane / (BN / 4), c4 = lane % (BN / 4);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void*)(smem + i * 1024), 16,
+                                                 (uint32_t)((row * g.ldr + 4 * c4) * 4), 0, 0, 0);
+      }
+#endif
+      wait_vm();
+      ring_barrier();
+      rl = reinterpret_cast<const float*>(smem);
+    }
+  }
+  if (role == 0) gemm_epilogue<S, C_BF16, FULL>(g, acc, m0, n0, split, rl);
 }
 
 template <int BM, int BN, int WGM, int NWM, int NWD, int NWL, bool TRANS, int ST, int TAG, bool Q4>

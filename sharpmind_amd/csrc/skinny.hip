@@ -736,10 +736,13 @@ int gemm_skinny(int M, int n, int K, const void* big, int64_t ldb, bool big_k, c
     return 1;
   }
   const int mt = ceil_div(M, MT), nk = K / BKT;
-  // splits: two workgroups per CU; fewer while the fp32 partials (written and read back)
-  // exceed a quarter of the bytes of Big, as long as every CU keeps a workgroup
+  // splits: one workgroup per CU (the engine step measured 0.3%, 0.7% and 0.9% faster than with
+  // 2, 4 and 8; SMHIP_SKINNY_WPC overrides for tuning runs); fewer while the fp32 partials
+  // (written and read back) exceed a quarter of the bytes of Big, as long as every CU keeps a
+  // workgroup
   const int cus = num_cus();
-  int S = std::max(1, ceil_div(2 * cus, mt));
+  static const int wpc = [] { const char* v = getenv("SMHIP_SKINNY_WPC"); return v ? atoi(v) : 1; }();
+  int S = std::max(1, ceil_div(wpc * cus, mt));
   S = std::min(S, std::max(1, nk / 2));
   while (S > 1 && (int64_t)S * M * n * 4 * 4 > (int64_t)M * K * 2 && mt * (S - 1) >= cus) S--;
   a.kps = ceil_div(nk, S);
