@@ -648,8 +648,15 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
       R_(rmsnorm_forward(sv.h_mid, w.norm2.data, e->bf ? nullptr : (float*)sv.xn2, e->bf ? (uint16_t*)sv.xn2 : nullptr,
                          sv.rinv2, T, d, c.norm_eps, s));
     R_(proj_forward(e, l, P_GU, sv.xn2, sv.gu, e->bf, nullptr, s, fused == 1));
-    R_(swiglu_fused_forward(sv.gu, sv.act, T, F, e->bf, s));
-    R_(proj_forward(e, l, P_D, sv.act, h_out, 0, sv.h_mid, s));  // h_out = h_mid + ffn
+    // bf16 LoRA: the SwiGLU also computes the down adapter's u = act A
+    fused = 0;
+    if (e->lora && e->bf && w.lat[P_D]) {
+      fused = swiglu_lora_u((const uint16_t*)sv.gu, (uint16_t*)sv.act, w.lat[P_D], e->nr[P_D], (uint16_t*)sv.u[P_D], T,
+                            F, s);
+      if (fused < 0) return fused;
+    }
+    if (!fused) R_(swiglu_fused_forward(sv.gu, sv.act, T, F, e->bf, s));
+    R_(proj_forward(e, l, P_D, sv.act, h_out, 0, sv.h_mid, s, fused == 1));  // h_out = h_mid + ffn
   }
   R_(rmsnorm_forward(e->h_fin, e->norm_f.data, e->bf ? nullptr : (float*)e->xnf, e->bf ? (uint16_t*)e->xnf : nullptr,
                      e->rinv_f, T, d, c.norm_eps, s));

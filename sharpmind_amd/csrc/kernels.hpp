@@ -91,6 +91,10 @@ struct BfTJob {
   int rows, cols;
 };
 int transpose_bf16_jobs(const BfTJob* jobs_dev, int njobs, int64_t max_elems, hipStream_t s);
+// SwiGLU forward (bf16 [gate | up] in, bf16 act out) fused with u = act A for a LoRA A given
+// transposed, At [n][F] (bf16); 1 = done, 0 = shapes unsupported (run them separately)
+int swiglu_lora_u(const uint16_t* gu, uint16_t* act, const uint16_t* At, int n, uint16_t* u, int T, int F,
+                  hipStream_t s);
 // RMSNorm forward (bf16 output) fused with u = xn A for a LoRA A given transposed, At [n][D] (bf16); 1 = done, 0 = shape
 // not supported (run rmsnorm_forward and the rank product instead)
 int rmsnorm_lora_u(const float* h, const float* w, float eps, uint16_t* xn, float* rinv, const uint16_t* At, int n,

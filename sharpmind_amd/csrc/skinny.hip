@@ -595,6 +595,69 @@ __global__ __launch_bounds__(512) void rmsnorm_lora_u_kernel(const float* __rest
   }
 }
 
+// SwiGLU forward fused with the LoRA down-projection of its output: act = silu(g) * u (bf16,
+// the arithmetic of swiglu_fused_forward, so act is bit-identical) and uo[t, :] = act[t, :] A
+// with A given transposed (At [n][F] bf16, n = 16 NB).  Same layout as rmsnorm_lora_u_kernel:
+// 16 rows per workgroup, 8 waves taking equal shares of F in 32-wide slices, each lane 8
+// consecutive columns of one row per slice (the MFMA A fragment), wave partials added in wave
+// order through LDS.
+template <int NB, int NS>  // NS = 32-wide slices per wave (F / 256), all loads issued up front
+__global__ __launch_bounds__(512) void swiglu_lora_u_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ act,
+                                                           const uint16_t* __restrict__ At, uint16_t* __restrict__ uo,
+                                                           int M, int F, int n) {
+  constexpr int NW = 8;
+  __shared__ __attribute__((aligned(16))) uint8_t red[NW * NB * 64 * 16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, rl = lane & 15;
+  const int m0 = blockIdx.x * 16, row = min(m0 + rl, M - 1);
+  const int kb = w * (F / NW);
+  const uint16_t* gr = gu + (int64_t)row * 2 * F;
+  floatx4 acc[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  uint4 gv[NS], uv[NS];
+#pragma unroll
+  for (int t = 0; t < NS; t++) {
+    gv[t] = *reinterpret_cast<const uint4*>(gr + kb + 32 * t + 8 * g);
+    uv[t] = *reinterpret_cast<const uint4*>(gr + F + kb + 32 * t + 8 * g);
+  }
+#pragma unroll
+  for (int t = 0; t < NS; t++) {
+    const int k0 = kb + 32 * t;
+    bf16x8 fb[NB];
+#pragma unroll
+    for (int j = 0; j < NB; j++) fb[j] = *reinterpret_cast<const bf16x8*>(At + (int64_t)(16 * j + rl) * F + k0 + 8 * g);
+    const uint32_t gw[4] = {gv[t].x, gv[t].y, gv[t].z, gv[t].w}, uw[4] = {uv[t].x, uv[t].y, uv[t].z, uv[t].w};
+    uint32_t pk[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float g0 = __uint_as_float(gw[i] << 16), g1 = __uint_as_float(gw[i] & 0xFFFF0000u);
+      const float u0 = __uint_as_float(uw[i] << 16), u1 = __uint_as_float(uw[i] & 0xFFFF0000u);
+      pk[i] = pack_bf2((g0 / (1.f + expf(-g0))) * u0, (g1 / (1.f + expf(-g1))) * u1);
+    }
+    const uint4 a4 = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    if (m0 + rl < M) *reinterpret_cast<uint4*>(act + (int64_t)(m0 + rl) * F + k0 + 8 * g) = a4;
+    const bf16x8 fa = __builtin_bit_cast(bf16x8, a4);
+#pragma unroll
+    for (int j = 0; j < NB; j++) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, fb[j], acc[j], 0, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < NB; j++) *reinterpret_cast<floatx4*>(red + ((w * NB + j) * 64 + lane) * 16) = acc[j];
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    floatx4 o = *reinterpret_cast<const floatx4*>(red + (j * 64 + lane) * 16);
+#pragma unroll
+    for (int q = 1; q < NW; q++) o += *reinterpret_cast<const floatx4*>(red + ((q * NB + j) * 64 + lane) * 16);
+    const int col = 16 * j + (lane & 15);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int r = m0 + 4 * (lane >> 4) + e;
+      if (r < M) uo[(int64_t)r * n + col] = f2bf(o[e]);
+    }
+  }
+}
+
 template <bool SMALLK, bool TRANS_OUT, bool C_BF16, int NW>
 static void launch_rows_nw(int nb, const Args& a, hipStream_t s) {
   const dim3 grid(ceil_div(a.M, 16)), block(64 * NW);
@@ -695,6 +758,34 @@ int rmsnorm_lora_u(const float* h, const float* w, float eps, uint16_t* xn, floa
     default: SMHIP_RLU(4) break;
   }
 #undef SMHIP_RLU
+  SMHIP_CHECK_LAUNCH();
+  return 1;
+}
+
+// Returns 1 when the fused kernel ran, 0 when the shapes do not fit it (the caller runs the
+// SwiGLU and the rank product separately).  gu [T][2F] = [gate | up] bf16, At [n][F].
+int swiglu_lora_u(const uint16_t* gu, uint16_t* act, const uint16_t* At, int n, uint16_t* u, int T, int F,
+                  hipStream_t s) {
+  using namespace sk;
+  if (T <= 0) return 1;
+  if (F % 256 || n % 16 || n < 16 || n > 64) return 0;
+  if (((uintptr_t)gu | (uintptr_t)act | (uintptr_t)At) % 16) return 0;
+  const dim3 grid(ceil_div(T, 16)), block(512);
+#define SMHIP_SLU(NB)                                                                                            \
+  switch (F / 256) {                                                                                             \
+    case 4: hipLaunchKernelGGL((swiglu_lora_u_kernel<NB, 4>), grid, block, 0, s, gu, act, At, u, T, F, n); break;   \
+    case 8: hipLaunchKernelGGL((swiglu_lora_u_kernel<NB, 8>), grid, block, 0, s, gu, act, At, u, T, F, n); break;   \
+    case 12: hipLaunchKernelGGL((swiglu_lora_u_kernel<NB, 12>), grid, block, 0, s, gu, act, At, u, T, F, n); break; \
+    case 16: hipLaunchKernelGGL((swiglu_lora_u_kernel<NB, 16>), grid, block, 0, s, gu, act, At, u, T, F, n); break; \
+    default: return 0;                                                                                           \
+  }
+  switch (n / 16) {
+    case 1: SMHIP_SLU(1) break;
+    case 2: SMHIP_SLU(2) break;
+    case 3: SMHIP_SLU(3) break;
+    default: SMHIP_SLU(4) break;
+  }
+#undef SMHIP_SLU
   SMHIP_CHECK_LAUNCH();
   return 1;
 }
