@@ -27,7 +27,11 @@ def _rnd(shape, rng):
     (256, 256, 256, 2, 2, 1), (4096, 1024, 1024, 2, 3, 1), (300, 136, 192, 2, 3, 1), (4096, 48, 1024, 2, 3, 8),
     (48, 1024, 4096, 3, 3, 8), (1000, 32, 2048, 3, 3, 13), (8192, 512, 128, 2, 2, 1), (130, 200, 100, 2, 2, 1),
     (64, 64, 64, 0, 1, 1), (4096, 1024, 1024, 2, 2, 0), (300, 136, 192, 2, 2, 0), (130, 1000, 64, 2, 2, 0),
-    (2048, 2048, 8192, 2, 2, 0), (4096, 3072, 1024, 2, 2, 0), (1000, 3072, 320, 2, 2, 0)])
+    (2048, 2048, 8192, 2, 2, 0), (4096, 3072, 1024, 2, 2, 0), (1000, 3072, 320, 2, 2, 0),
+    # row-contiguous operands staged as stored and read transposed: the weight-gradient shapes
+    # (auto split), ragged edges, the 256x192 and 256x256 tiles with a row-contiguous B
+    (4096, 1024, 4096, 3, 3, 0), (1024, 2048, 4096, 3, 3, 0), (1000, 200, 320, 3, 3, 2), (600, 192, 256, 3, 3, 1),
+    (4096, 3072, 1024, 2, 3, 0), (4096, 2048, 1024, 2, 3, 0), (2048, 4096, 512, 2, 3, 0), (520, 328, 448, 2, 3, 0)])
 @pytest.mark.parametrize("c_bf16", [0, 1])
 def test_gemm_modes(dev, M, N, K, am, bm, split, c_bf16):
     rng = np.random.default_rng(M + N + K + am + bm)
