@@ -274,7 +274,12 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_fwd_kernel(const uint16_t
         for (int e = 0; e < 16; e++) mx = fmaxf(mx, sacc[j][e]);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(m, mx * sl2);
+    // lazy rescaling: the reference max moves only when the running max grows by more than 8
+    // (log2 units), so p <= 2^8 and the O rescale below is skipped for most key blocks; m only
+    // has to be a common reference for p, l and O, and the final O / l and LSE = m + log2 l are
+    // unchanged in exact arithmetic
+    const float mc = fmaxf(m, mx * sl2);
+    const float mnew = mc > m + 8.f ? mc : m;
     const float alpha = fexp2(m - mnew);
     float rs = 0.f;
 #pragma unroll
@@ -288,7 +293,7 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_fwd_kernel(const uint16_t
     rs += __shfl_xor(rs, 32, 64);
     l = l * alpha + rs;
     m = mnew;
-    // rescale only when some query's running max moved (alpha == 1 multiplies are exact no-ops)
+    // rescale only when some query's reference max moved (alpha == 1 multiplies are exact no-ops)
     if (__any(alpha != 1.f)) {
 #pragma unroll
       for (int i = 0; i < D / 32; i++)
@@ -396,7 +401,12 @@ __global__ __launch_bounds__(PAIR ? 512 : 256) void fa_fwd128_kernel(const uint1
         for (int e = 0; e < 16; e++) mx = fmaxf(mx, sacc[j][e]);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(m, mx * sl2);
+    // lazy rescaling: the reference max moves only when the running max grows by more than 8
+    // (log2 units), so p <= 2^8 and the O rescale below is skipped for most key blocks; m only
+    // has to be a common reference for p, l and O, and the final O / l and LSE = m + log2 l are
+    // unchanged in exact arithmetic
+    const float mc = fmaxf(m, mx * sl2);
+    const float mnew = mc > m + 8.f ? mc : m;
     const float alpha = fexp2(m - mnew);
     float rs = 0.f;
 #pragma unroll
