@@ -245,6 +245,18 @@ int gemm_bf16_fast(const GemmArgs& g, hipStream_t s) {
     if (tiles < target && !w8) {
       sp = (int)std::min<int64_t>((target + tiles - 1) / tiles, nk / (sk ? 2 : 8));
       sp = std::max(1, std::min(sp, 64));
+      if (!sk) {
+        // fewest rounds of resident workgroups per unit of K work; ties go to fewer splits (less
+        // partial traffic).  E.g. 192 tiles: 2 splits fill 384 of 512 slots in one round, 3 need
+        // two rounds (measured 46 against 53 us for the down-projection weight gradient)
+        int best = 1;
+        double best_c = 1e300;
+        for (int c = 1; c <= sp; c++) {
+          const double cost = (double)((tiles * c + target - 1) / target) / c;
+          if (cost < best_c * 0.999) { best_c = cost; best = c; }
+        }
+        sp = best;
+      }
       while (sp > 1 && (int64_t)sp * g.M * g.N * 4 > ((int64_t)64 << 20)) sp--;
     }
     a.kps = ceil_div(nk, sp);
