@@ -590,6 +590,13 @@ static int proj_backward(Engine* e, int l, int p, const void* dY, const float* d
   return gemm(g, s);
 }
 
+// attention's V: in place inside the bf16 q|k|v projection output (row pitch nqkv), else the
+// separate copy the QK-norm/RoPE pass writes
+static const uint16_t* vsrc(const Engine* e, const Saved& sv) {
+  return e->qkv_bf ? (const uint16_t*)sv.qkv + e->qd + e->kvd : (const uint16_t*)sv.v;
+}
+static int64_t vld(const Engine* e) { return e->qkv_bf ? e->nqkv : e->kvd; }
+
 // ------------------------------------------------------------------ step
 static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels, hipStream_t s) {
   const smhip_model_config& c = e->c;
@@ -627,12 +634,13 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
       R_(rmsnorm_forward(sv.h_in, w.norm1.data, e->bf ? nullptr : (float*)sv.xn1, e->bf ? (uint16_t*)sv.xn1 : nullptr,
                          sv.rinv1, T, d, c.norm_eps, s));
     R_(proj_forward(e, l, P_QKV, sv.xn1, sv.qkv, e->qkv_bf, nullptr, s, fused == 1));
-    R_(qkv_prep_forward(sv.qkv, e->qkv_bf, sv.q, sv.k, sv.v, sv.rinv_qk, c.qk_norm ? w.qn.data : nullptr,
+    // bf16 q|k|v projections: attention reads V in place (row pitch nqkv), no copy
+    R_(qkv_prep_forward(sv.qkv, e->qkv_bf, sv.q, sv.k, e->qkv_bf ? nullptr : sv.v, sv.rinv_qk, c.qk_norm ? w.qn.data : nullptr,
                         c.qk_norm ? w.kn.data : nullptr, e->cosT, e->sinT, T, c.seq, Hq, Hkv, D, c.qk_norm,
                         c.rope_neox, c.norm_eps, e->bf, s));
     if (e->bf) {
-      R_(flash_forward((const uint16_t*)sv.q, (const uint16_t*)sv.k, (const uint16_t*)sv.v, (uint16_t*)sv.o, sv.lse,
-                       c.batch, c.seq, Hq, Hkv, D, e->qd, e->kvd, e->kvd, e->qd, s));
+      R_(flash_forward((const uint16_t*)sv.q, (const uint16_t*)sv.k, vsrc(e, sv), (uint16_t*)sv.o, sv.lse, c.batch,
+                       c.seq, Hq, Hkv, D, e->qd, e->kvd, vld(e), e->qd, s));
     } else {
       R_(attention_forward_probs((const float*)sv.q, (const float*)sv.k, (const float*)sv.v, sv.probs, (float*)sv.o,
                                  c.batch, c.seq, Hq, Hkv, D, s));
@@ -725,9 +733,9 @@ static int forward_backward(Engine* e, const int32_t* ids, const int32_t* labels
     if (e->bf) {
       // dK / dV stay per query head; the QK-norm / RoPE backward sums each GQA group as it reads
       // them.  dQ and the partials are bf16: their one consumer rounds its output to bf16.
-      R_(flash_backward((const uint16_t*)sv.q, (const uint16_t*)sv.k, (const uint16_t*)sv.v, (const uint16_t*)sv.o,
+      R_(flash_backward((const uint16_t*)sv.q, (const uint16_t*)sv.k, vsrc(e, sv), (const uint16_t*)sv.o,
                         (const uint16_t*)e->dO, sv.lse, e->dq, nullptr, nullptr, c.batch, c.seq, Hq, Hkv, D, e->qd,
-                        e->kvd, e->kvd, e->qd, e->qd, e->qd, e->kvd, e->kvd, e->flash_ws, s, 1));
+                        e->kvd, vld(e), e->qd, e->qd, e->qd, e->kvd, e->kvd, e->flash_ws, s, 1));
       flash_backward_partials(e->flash_ws, c.batch, c.seq, Hq, D, &dk, &dv);
       kv_grp = Hq / Hkv;
     } else {

@@ -254,6 +254,8 @@ __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
   // partners (i, i + D/2) sit in lanes l and l ^ 1
   const int eo = (l & 1) * P + E * (l >> 1);
   const int H = Hq + 2 * Hkv, nqkv = H * D;
+  // vo null: V is read where the projection wrote it (no copy), only q and k rows are processed
+  const int Hl = vo ? H : Hq + Hkv;
   // workgroup per token: the half-waves take heads hw, hw + 8, ...; the lane's RoPE factors
   // depend only on the lane and the position, so they are loaded once per token
   for (int t = blockIdx.x; t < T; t += gridDim.x) {
@@ -271,15 +273,15 @@ __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
       }
     }
     const TQ* xt = qkv + (int64_t)t * nqkv;
-    for (int h0 = hw; h0 < H; h0 += 8 * R) {
+    for (int h0 = hw; h0 < Hl; h0 += 8 * R) {
       float v[R][E];
 #pragma unroll
       for (int r = 0; r < R; r++)
-        if (h0 + 8 * r < H) ldE<E>(xt + (h0 + 8 * r) * D + eo, v[r]);
+        if (h0 + 8 * r < Hl) ldE<E>(xt + (h0 + 8 * r) * D + eo, v[r]);
 #pragma unroll
       for (int r = 0; r < R; r++) {
         const int hh = h0 + 8 * r;
-        if (hh >= H) break;
+        if (hh >= Hl) break;
         if (hh >= Hq + Hkv) {
           stE<E>(vo + (int64_t)t * Hkv * D + (hh - Hq - Hkv) * D + eo, v[r]);
           continue;
@@ -456,6 +458,7 @@ int qkv_prep_forward(const void* qkv, int qkv_bf16, void* q, void* k, void* v, f
                      int D, int qk_norm, int neox, float eps, int bf16, hipStream_t s) {
   SMHIP_REQUIRE(D <= 128 && D % 2 == 0, "qkv prep: head_dim must be even and <= 128");
   const int64_t rows = (int64_t)T * (Hq + 2 * Hkv);
+  SMHIP_REQUIRE(v || (D == 128 || D == 64), "qkv prep: v may be omitted only for head_dim 64 or 128");
   if (D == 128 || D == 64) {
     const int gv = (int)std::min<int64_t>(T, (int64_t)num_cus() * 8);  // workgroup per token
 #define SMHIP_QKV_FWD(DD, TT, TQ) \
