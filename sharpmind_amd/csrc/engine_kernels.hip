@@ -191,15 +191,24 @@ template <int E> struct VecF;
 template <> struct VecF<2> { typedef float2 T; };
 template <> struct VecF<4> { typedef float4 T; };
 template <int E> __device__ __forceinline__ void ldE(const float* p, float* v) {
-  const typename VecF<E>::T t = *reinterpret_cast<const typename VecF<E>::T*>(p);
-  const float* f = reinterpret_cast<const float*>(&t);
+  if constexpr (E == 8) {
+    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    return;
+  } else {
+    const typename VecF<E>::T t = *reinterpret_cast<const typename VecF<E>::T*>(p);
+    const float* f = reinterpret_cast<const float*>(&t);
 #pragma unroll
-  for (int i = 0; i < E; i++) v[i] = f[i];
+    for (int i = 0; i < E; i++) v[i] = f[i];
+  }
 }
 // E bf16 values (4 or 8 bytes) widened to fp32
 template <int E> __device__ __forceinline__ void ldE(const uint16_t* p, float* v) {
   uint32_t w[E / 2];
-  if constexpr (E == 4) {
+  if constexpr (E == 8) {
+    const uint4 t = *reinterpret_cast<const uint4*>(p);
+    w[0] = t.x; w[1] = t.y; w[2] = t.z; w[3] = t.w;
+  } else if constexpr (E == 4) {
     const uint2 t = *reinterpret_cast<const uint2*>(p);
     w[0] = t.x;
     w[1] = t.y;
@@ -213,7 +222,10 @@ template <int E> __device__ __forceinline__ void ldE(const uint16_t* p, float* v
   }
 }
 template <int E, typename TA> __device__ __forceinline__ void stE(TA* p, const float* v) {
-  if constexpr (sizeof(TA) == 4) {
+  if constexpr (sizeof(TA) == 4 && E == 8) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  } else if constexpr (sizeof(TA) == 4) {
     typename VecF<E>::T t;
     float* f = reinterpret_cast<float*>(&t);
 #pragma unroll
@@ -223,7 +235,8 @@ template <int E, typename TA> __device__ __forceinline__ void stE(TA* p, const f
     uint32_t w[E / 2];
 #pragma unroll
     for (int i = 0; i < E / 2; i++) w[i] = pack_bf2(v[2 * i], v[2 * i + 1]);
-    if constexpr (E == 4) *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+    if constexpr (E == 8) *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    else if constexpr (E == 4) *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
     else *reinterpret_cast<uint32_t*>(p) = w[0];
   }
 }
@@ -233,6 +246,15 @@ __device__ __forceinline__ float dpp_xor1(float v) {
 }
 // sum over the 32 lanes of a half wave: quad permutes (xor 1, xor 2), the 8- and 16-lane mirrors
 // by DPP, one cross-row shuffle; every lane ends with the same bits
+// sum over the 16 lanes of a row group (the DPP steps of half_sum without the xor-16 shuffle)
+__device__ __forceinline__ float quarter_sum(float v) {
+  v += dpp_xor1(v);
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, true));
+  return v;
+}
+template <int L> __device__ __forceinline__ float group_sum(float v);
 __device__ __forceinline__ float half_sum(float v) {
   v += dpp_xor1(v);
   v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
@@ -241,6 +263,8 @@ __device__ __forceinline__ float half_sum(float v) {
   v += __shfl_xor(v, 16, 64);
   return v;
 }
+template <> __device__ __forceinline__ float group_sum<32>(float v) { return half_sum(v); }
+template <> __device__ __forceinline__ float group_sum<16>(float v) { return quarter_sum(v); }
 
 template <int D, typename TA, typename TQ>
 __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
@@ -319,15 +343,17 @@ __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
   }
 }
 
-template <int D, typename TA, typename TQ, typename TG>
+// L = lanes per head row: 32 (E = D/32 elements per lane) or 16 (E = D/16: 16-byte bf16 accesses
+// at D = 128, 16 row groups per workgroup)
+template <int D, typename TA, typename TQ, typename TG, int L = 32>
 __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
     const TG* __restrict__ dq, const TG* __restrict__ dk, const TG* __restrict__ dv,
     const TQ* __restrict__ qkv, const float* __restrict__ rinv, const float* __restrict__ wq,
     const float* __restrict__ wk, const float* __restrict__ cosT, const float* __restrict__ sinT,
     TA* __restrict__ dqkv, float* __restrict__ part, int T, int S, int Hq, int Hkv, int qk_norm, int neox,
     int kv_grp) {
-  constexpr int E = D / 32, P = D / 2;
-  const int l = threadIdx.x & 31, hw = threadIdx.x >> 5;  // half-wave 0..7
+  constexpr int E = D / L, P = D / 2, NG = 256 / L;
+  const int l = threadIdx.x & (L - 1), hw = threadIdx.x / L;  // row group 0 .. NG-1
   const int eo = (l & 1) * P + E * (l >> 1);  // as in the forward: NeoX partners in lanes l, l ^ 1
   // kv_grp > 0: dk / dv are the attention backward's per-query-head partials [T, Hq, D]; a KV
   // head's gradient is the sum of its kv_grp query heads, added in ascending head order
@@ -374,11 +400,11 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
         sn[i] = sn[i + 1] = sinT[(int64_t)pos * P + p];
       }
     }
-    for (int h0 = hw; h0 < H; h0 += 8 * R) {
+    for (int h0 = hw; h0 < H; h0 += NG * R) {
       float g[R][E], x[R][E], ri[R];
 #pragma unroll
       for (int r = 0; r < R; r++) {
-        const int hh = h0 + 8 * r;
+        const int hh = h0 + NG * r;
         if (hh >= H) break;
         if (hh >= Hq + Hkv) {
           ld_kv(dv, t, hh - Hq - Hkv, g[r]);
@@ -393,7 +419,7 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
       }
 #pragma unroll
       for (int r = 0; r < R; r++) {
-        const int hh = h0 + 8 * r;
+        const int hh = h0 + NG * r;
         if (hh >= H) break;
         TA* dst = dqkv + (int64_t)t * nqkv + hh * D + eo;
         if (hh >= Hq + Hkv) {
@@ -429,7 +455,7 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
           if (isq) aq[i] += gr[i] * xn[i];
           else ak[i] += gr[i] * xn[i];
         }
-        dot = half_sum(dot) / (float)D;
+        dot = group_sum<L>(dot) / (float)D;
         float o[E];
 #pragma unroll
         for (int i = 0; i < E; i++) o[i] = ri[r] * (gr[i] * w[i] - xn[i] * dot);
@@ -437,8 +463,8 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
       }
     }
   }
-  if (part) {  // block partial of dw: sum the 8 half-waves in a fixed order
-    __shared__ float sh[8][2][D];
+  if (part) {  // block partial of dw: sum the NG row groups in a fixed order
+    __shared__ float sh[NG][2][D];
 #pragma unroll
     for (int i = 0; i < E; i++) {
       sh[hw][0][eo + i] = aq[i];
@@ -447,7 +473,7 @@ __global__ __launch_bounds__(256) void qkv_prep_bwd_vec_kernel(
     __syncthreads();
     for (int c = threadIdx.x; c < 2 * D; c += 256) {
       float acc = 0.f;
-      for (int h = 0; h < 8; h++) acc += sh[h][c / D][c % D];
+      for (int h = 0; h < NG; h++) acc += sh[h][c / D][c % D];
       part[(int64_t)blockIdx.x * 2 * D + c] = acc;
     }
   }
@@ -514,7 +540,11 @@ int qkv_prep_backward(const void* dq_, const void* dk_, const void* dv_, int gra
   else                                                                                                             \
     hipLaunchKernelGGL((qkv_prep_bwd_vec_kernel<DD, TT, TQ, float>), dim3(g), dim3(256), 0, s, dq, dk, dv,         \
                        (const TQ*)qkv, rinv, wq, wk, cosT, sinT, (TT*)dqkv, part, T, S, Hq, Hkv, qk_norm, neox, kv_grp)
-    if (qkv_bf16) { if (D == 128) SMHIP_QKV_BWD(128, uint16_t, uint16_t); else SMHIP_QKV_BWD(64, uint16_t, uint16_t); }
+    if (qkv_bf16 && grads_bf16 && D == 128)  // 16 lanes per row: 16-byte accesses
+      hipLaunchKernelGGL((qkv_prep_bwd_vec_kernel<128, uint16_t, uint16_t, uint16_t, 16>), dim3(g), dim3(256), 0, s,
+                         (const uint16_t*)dq_, (const uint16_t*)dk_, (const uint16_t*)dv_, (const uint16_t*)qkv, rinv,
+                         wq, wk, cosT, sinT, (uint16_t*)dqkv, part, T, S, Hq, Hkv, qk_norm, neox, kv_grp);
+    else if (qkv_bf16) { if (D == 128) SMHIP_QKV_BWD(128, uint16_t, uint16_t); else SMHIP_QKV_BWD(64, uint16_t, uint16_t); }
     else if (D == 128) { if (bf16) SMHIP_QKV_BWD(128, uint16_t, float); else SMHIP_QKV_BWD(128, float, float); }
     else { if (bf16) SMHIP_QKV_BWD(64, uint16_t, float); else SMHIP_QKV_BWD(64, float, float); }
 #undef SMHIP_QKV_BWD
