@@ -266,14 +266,16 @@ __device__ __forceinline__ float half_sum(float v) {
 template <> __device__ __forceinline__ float group_sum<32>(float v) { return half_sum(v); }
 template <> __device__ __forceinline__ float group_sum<16>(float v) { return quarter_sum(v); }
 
-template <int D, typename TA, typename TQ>
+// L = lanes per head row (32, or 16 for 16-byte bf16 accesses at D = 128)
+template <int D, typename TA, typename TQ, int L = 32>
 __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
     const TQ* __restrict__ qkv, TA* __restrict__ qo, TA* __restrict__ ko, TA* __restrict__ vo,
     float* __restrict__ rinv, const float* __restrict__ wq, const float* __restrict__ wk,
     const float* __restrict__ cosT, const float* __restrict__ sinT, int T, int S, int Hq, int Hkv,
     int qk_norm, int neox, float eps) {
-  constexpr int E = D / 32, P = D / 2, R = 4;  // R rows in flight per half-wave
-  const int l = threadIdx.x & 31, hw = threadIdx.x >> 5;
+  constexpr int E = D / L, P = D / 2, NG = 256 / L;
+  constexpr int R = L == 32 ? 4 : 2;  // rows in flight per row group
+  const int l = threadIdx.x & (L - 1), hw = threadIdx.x / L;
   // lane l holds elements eo .. eo + E - 1 of a head row, the halves interleaved so that NeoX
   // partners (i, i + D/2) sit in lanes l and l ^ 1
   const int eo = (l & 1) * P + E * (l >> 1);
@@ -297,14 +299,14 @@ __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
       }
     }
     const TQ* xt = qkv + (int64_t)t * nqkv;
-    for (int h0 = hw; h0 < Hl; h0 += 8 * R) {
+    for (int h0 = hw; h0 < Hl; h0 += NG * R) {
       float v[R][E];
 #pragma unroll
       for (int r = 0; r < R; r++)
-        if (h0 + 8 * r < Hl) ldE<E>(xt + (h0 + 8 * r) * D + eo, v[r]);
+        if (h0 + NG * r < Hl) ldE<E>(xt + (h0 + NG * r) * D + eo, v[r]);
 #pragma unroll
       for (int r = 0; r < R; r++) {
-        const int hh = h0 + 8 * r;
+        const int hh = h0 + NG * r;
         if (hh >= Hl) break;
         if (hh >= Hq + Hkv) {
           stE<E>(vo + (int64_t)t * Hkv * D + (hh - Hq - Hkv) * D + eo, v[r]);
@@ -316,7 +318,7 @@ __global__ __launch_bounds__(256) void qkv_prep_fwd_vec_kernel(
           float ss = 0.f;
 #pragma unroll
           for (int i = 0; i < E; i++) ss += v[r][i] * v[r][i];
-          ss = half_sum(ss);
+          ss = group_sum<L>(ss);
           const float ri = 1.f / sqrtf(ss / (float)D + eps);
           if (l == 0) rinv[(int64_t)t * (Hq + Hkv) + hh] = ri;
 #pragma unroll
@@ -491,7 +493,11 @@ int qkv_prep_forward(const void* qkv, int qkv_bf16, void* q, void* k, void* v, f
   hipLaunchKernelGGL((qkv_prep_fwd_vec_kernel<DD, TT, TQ>), dim3(gv), dim3(256), 0, s, (const TQ*)qkv, (TT*)q, (TT*)k, (TT*)v, rinv, wq, wk, cosT, sinT, T, S, Hq, Hkv, qk_norm, neox, eps)
     if (qkv_bf16) {
       SMHIP_REQUIRE(bf16, "qkv prep: bf16 projections need bf16 outputs");
-      if (D == 128) SMHIP_QKV_FWD(128, uint16_t, uint16_t); else SMHIP_QKV_FWD(64, uint16_t, uint16_t);
+      if (D == 128)  // 16 lanes per row: 16-byte accesses
+        hipLaunchKernelGGL((qkv_prep_fwd_vec_kernel<128, uint16_t, uint16_t, 16>), dim3(gv), dim3(256), 0, s,
+                           (const uint16_t*)qkv, (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, rinv, wq, wk, cosT, sinT, T,
+                           S, Hq, Hkv, qk_norm, neox, eps);
+      else SMHIP_QKV_FWD(64, uint16_t, uint16_t);
     } else if (D == 128) { if (bf16) SMHIP_QKV_FWD(128, uint16_t, float); else SMHIP_QKV_FWD(128, float, float); }
     else { if (bf16) SMHIP_QKV_FWD(64, uint16_t, float); else SMHIP_QKV_FWD(64, float, float); }
 #undef SMHIP_QKV_FWD
